@@ -1,0 +1,427 @@
+// Planner, pack and 3D RoPE kernels for gfx950.
+//
+// The planner runs on the device: one workgroup walks the (chunk, head)
+// pairs of a layer call, emits each pair's ordered segment list and
+// computes the global offsets with a block-wide exclusive scan, so the plan
+// never leaves the GPU (the reference builds it on the host after three
+// blocking device-to-host copies, mega_plan.cc:557-568).
+//
+// The pack kernel is a persistent gather: each work item is (segment,
+// 64-token tile); 16 lanes move one 256-byte K row with 16-byte loads, the
+// same lanes rotate their 4 complex pairs in registers, V and positions are
+// copied alongside.
+
+#include "pkv_common.h"
+
+namespace pkv {
+
+// ---------------------------------------------------------------------------
+// dynamic-RoPE time remaps (mega_plan.cc:63-114, rope.py:86-134)
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int64_t map_sink_time(int64_t t, int mode, int cmin, int cmax, int lag) {
+  if (mode == 1) {
+    int64_t d = t;
+    if (d < cmin) d = cmin;
+    if (d > cmax) d = cmax;
+    const int64_t out = t - d;
+    return out < 0 ? 0 : out;
+  }
+  const int64_t out = t - lag;
+  return out < 0 ? 0 : out;
+}
+
+constexpr int kMaxPlanChunks = 64;
+constexpr int kPlanThreads = 256;
+constexpr int kMaxPlanPairs = 4096;
+
+struct PlanParams {
+  int H, S, FSEQ, max_sink, max_middle, max_recent, MMB, C;
+  int64_t t[kMaxPlanChunks];
+  int64_t sync_t[kMaxPlanChunks];
+};
+
+// Segment emission for one (chunk c, head h), in the reference order sink ->
+// recent -> middle (Wave bucket of the current phase, or the Anchor/lag
+// ring in slot order) -> merge anchors (mega_plan.cc:133-264).  Offsets are
+// relative to the pair; the caller adds the pair's global base.
+__device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int64_t *vc_h,
+                             const int32_t *mtc_h, int c, int h, int base, const pkv_plan_out &o) {
+  const int S = p.S;
+  const int64_t t_c = p.t[c], sync_t = p.sync_t[c];
+  const int thresh = s.sink_capacity;
+  const int recent_min_t = 0x7fffffff;
+  int32_t run = 0;
+  int fp = 0;
+  auto put = [&](int kind, int sg, int len, int64_t traw, int64_t tremap) {
+    const int i = base + fp;
+    o.src_kind[i] = kind;
+    o.src_slot_global[i] = sg;
+    o.seg_lengths[i] = len;
+    o.dst_token_offsets[i] = run;
+    o.anchor_t_raw[i] = traw;
+    o.anchor_t_remap[i] = tremap;
+    run += len;
+    ++fp;
+  };
+  const int n_sink_raw = static_cast<int>(vc_h[0]);
+  const int n_sink = (thresh > 0 && thresh < n_sink_raw) ? thresh : n_sink_raw;
+  for (int q = 0; q < n_sink && q < p.max_sink; ++q) put(PKV_SEG_SINK, h * p.max_sink + q, p.FSEQ, q, sync_t);
+  const int n_recent = static_cast<int>(vc_h[2]);
+  for (int r = 0; r < n_recent && r < p.max_recent; ++r) put(PKV_SEG_RECENT, h * p.max_recent + r, p.FSEQ, -1, -1);
+  if (s.kind == SK_CYCLIC) {
+    const int period = s.period > 0 ? s.period : 1;
+    const int bucket_cap = s.bucket_cap > 0 ? s.bucket_cap : 1;
+    const int phase = static_cast<int>(((t_c % period) + period) % period);
+    const int b0 = phase * kMaxBucket;
+    const int b1 = b0 + (bucket_cap < kMaxBucket ? bucket_cap : kMaxBucket);
+    for (int i = b0; i < b1 && i < kMaxPhase * kMaxBucket; ++i) {
+      if (s.cyclic_slot[i] < 0) continue;
+      if (s.cyclic_t[i] < thresh) continue;
+      if (s.cyclic_t[i] >= recent_min_t) continue;
+      put(PKV_SEG_MIDDLE, h * p.max_middle + i, p.FSEQ, s.cyclic_t[i], sync_t);
+      if (fp >= S) break;
+    }
+  } else if (s.kind == SK_STRIDE || s.kind == SK_LAG) {
+    const int tc = s.tkey_count;
+    for (int i = 0; i < tc && i < kMaxTKeyed; ++i) {
+      if (s.tkey_t[i] < thresh) continue;
+      if (s.tkey_t[i] >= recent_min_t) continue;
+      put(PKV_SEG_MIDDLE, h * p.max_middle + i, p.FSEQ, s.tkey_t[i], s.kind == SK_STRIDE ? sync_t : -1);
+      if (fp >= S) break;
+    }
+  }
+  if (s.kind == SK_MERGE) {
+    const int mcc = s.merge_completed_count;
+    for (int i = 0; i < mcc && i < kMaxMergeBlocks; ++i) {
+      const int slot = s.merge_completed_slot[i];
+      if (slot < 0 || slot >= p.MMB) continue;
+      if (s.merge_completed_start_t[i] <= 0) continue;
+      if (s.merge_completed_end_t[i] >= recent_min_t) continue;
+      const int32_t tok = mtc_h[slot];
+      if (tok <= 0) continue;
+      if (fp >= S) break;
+      put(PKV_SEG_MERGE, h * p.MMB + slot, tok, 0, s.merge_completed_median_t[i]);
+    }
+  }
+  for (int i = fp; i < S; ++i) {
+    const int j = base + i;
+    o.src_kind[j] = PKV_SEG_INACTIVE;
+    o.src_slot_global[j] = 0;
+    o.seg_lengths[j] = 0;
+    o.dst_token_offsets[j] = 0;
+    o.anchor_t_raw[j] = -1;
+    o.anchor_t_remap[j] = -1;
+  }
+  return run;
+}
+
+__global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const HeadState *states,
+                                                            const int64_t *vc, const int32_t *mtc,
+                                                            pkv_plan_out o, int32_t *total_out) {
+  __shared__ int32_t len[kMaxPlanPairs];
+  __shared__ int32_t part[kPlanThreads];
+  const int tid = threadIdx.x;
+  const int pairs = p.C * p.H;
+  for (int q = tid; q < pairs; q += blockDim.x) {
+    const int c = q / p.H, h = q % p.H;
+    len[q] = emit_pair(p, states[h], vc + h * 3, mtc + h * p.MMB, c, h, q * p.S, o);
+  }
+  __syncthreads();
+  // exclusive scan of len[0..pairs): contiguous chunk per thread, then a
+  // Hillis-Steele scan over the per-thread totals
+  const int per = (pairs + kPlanThreads - 1) / kPlanThreads;
+  const int q0 = tid * per, q1 = min(q0 + per, pairs);
+  int32_t acc = 0;
+  for (int q = q0; q < q1; ++q) acc += len[q];
+  part[tid] = acc;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int32_t v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int32_t base = part[tid] - acc;
+  for (int q = q0; q < q1; ++q) {
+    const int32_t l = len[q];
+    len[q] = base;
+    base += l;
+  }
+  __syncthreads();
+  if (tid == 0) o.cu_seqlens_k[0] = 0;
+  for (int q = tid; q < pairs; q += blockDim.x) {
+    const int32_t b = len[q];
+    for (int i = 0; i < p.S; ++i) {
+      const int j = q * p.S + i;
+      if (o.src_kind[j] >= 0) o.dst_token_offsets[j] += b;
+    }
+    const int32_t end = (q + 1 < pairs) ? len[q + 1] : part[kPlanThreads - 1];
+    o.cu_seqlens_k[q + 1] = end;
+  }
+  if (tid == 0 && total_out) *total_out = part[kPlanThreads - 1];
+}
+
+// ---------------------------------------------------------------------------
+// 3D RoPE on one 16-byte chunk (8 bf16 = 4 complex pairs) of a K row
+// (pyramidkv_pack.cu:114-161, rope.py:18-68)
+// ---------------------------------------------------------------------------
+struct Rope {
+  const float *ft, *fy, *fx;
+  int ft_rows, ft_cols, fy_rows, fy_cols, fx_rows, fx_cols;
+};
+
+__device__ inline int clamp_row(int64_t v, int rows) {
+  int r = static_cast<int>(v);
+  if (r < 0) r = 0;
+  if (r >= rows) r = rows - 1;
+  return r;
+}
+
+// The complex product is evaluated as (kr*fr - ki*fi, kr*fi + ki*fr) with
+// every product and sum individually rounded (explicit round-to-nearest
+// operations, no FMA contraction), the formula the CPU restatement uses;
+// results round to bf16 RNE.
+__device__ inline uint4 rope_chunk(uint4 raw, int chunk, int64_t t, int64_t y, int64_t x, const Rope &r) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t o[4];
+  const int rt = clamp_row(t, r.ft_rows), ry = clamp_row(y, r.fy_rows), rx = clamp_row(x, r.fx_rows);
+  const int fy_end = r.ft_cols + r.fy_cols;
+  for (int e = 0; e < 4; ++e) {
+    const int pidx = chunk * 4 + e;
+    const float *tab;
+    if (pidx < r.ft_cols)
+      tab = r.ft + (static_cast<int64_t>(rt) * r.ft_cols + pidx) * 2;
+    else if (pidx < fy_end)
+      tab = r.fy + (static_cast<int64_t>(ry) * r.fy_cols + (pidx - r.ft_cols)) * 2;
+    else
+      tab = r.fx + (static_cast<int64_t>(rx) * r.fx_cols + (pidx - fy_end)) * 2;
+    const float2 f = *reinterpret_cast<const float2 *>(tab);
+    const float kr = bf16_to_f32(static_cast<uint16_t>(w[e] & 0xffff));
+    const float ki = bf16_to_f32(static_cast<uint16_t>(w[e] >> 16));
+    const float a = __fmul_rn(kr, f.x), b = __fmul_rn(ki, f.y);
+    const float c = __fmul_rn(kr, f.y), d = __fmul_rn(ki, f.x);
+    o[e] = pack_bf16x2(__fsub_rn(a, b), __fadd_rn(c, d));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__device__ inline uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
+
+// ---------------------------------------------------------------------------
+// pack
+// ---------------------------------------------------------------------------
+constexpr int kPackTok = 64;
+constexpr int kPackThreads = 256;
+
+struct PackArgs {
+  const uint16_t *k[4], *v[4];
+  const int64_t *pos[4];
+  int64_t slots[4];
+  uint16_t *k_out, *v_out;
+  int64_t *pos_out;
+  const int32_t *kind, *sg, *len, *dst;
+  const int64_t *tremap;
+  Rope rope;
+  int fuse;  // rope tables + tremap present
+  int n_seg, tiles_per_seg, FSEQ, MTPA, D;
+  int64_t capacity;
+};
+
+__global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
+  const int items = a.n_seg * a.tiles_per_seg;
+  const int cpt = a.D / 8;
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    const int seg = it / a.tiles_per_seg, tile = it % a.tiles_per_seg;
+    const int kind = a.kind[seg];
+    if (kind < 0 || kind > 3) continue;
+    const int len = a.len[seg];
+    const int tok0 = tile * kPackTok;
+    if (len <= 0 || tok0 >= len) continue;
+    const int64_t sg = a.sg[seg];
+    const int64_t dst = a.dst[seg];
+    if (sg < 0 || sg >= a.slots[kind] || dst < 0 || dst + len > a.capacity || !a.k[kind]) continue;
+    const int stride = (kind == PKV_SEG_MERGE) ? a.MTPA : a.FSEQ;
+    if (len > stride) continue;
+    const uint16_t *sk = a.k[kind] + sg * stride * a.D;
+    const uint16_t *sv = a.v[kind] + sg * stride * a.D;
+    const int64_t *sp = a.pos[kind] ? a.pos[kind] + sg * stride * 3 : nullptr;
+    uint16_t *ok = a.k_out + dst * a.D;
+    uint16_t *ov = a.v_out + dst * a.D;
+    const bool rope = a.fuse && sp;
+    const int64_t tr = rope ? a.tremap[seg] : -1;
+    const int ntok = min(kPackTok, len - tok0);
+    for (int i = threadIdx.x; i < ntok * cpt; i += blockDim.x) {
+      const int tok = tok0 + i / cpt, ch = i % cpt;
+      const int64_t e = static_cast<int64_t>(tok) * a.D + ch * 8;
+      uint4 kk = ld16(sk + e);
+      const uint4 vv = ld16(sv + e);
+      if (rope) {
+        const int64_t *pp = sp + static_cast<int64_t>(tok) * 3;
+        const int64_t t = tr >= 0 ? tr : pp[0];
+        kk = rope_chunk(kk, ch, t, pp[1], pp[2], a.rope);
+      }
+      st16(ok + e, kk);
+      st16(ov + e, vv);
+    }
+    if (a.pos_out && sp) {
+      int64_t *op = a.pos_out + dst * 3;
+      for (int i = threadIdx.x; i < ntok * 3; i += blockDim.x) {
+        const int64_t e = static_cast<int64_t>(tok0) * 3 + i;
+        op[e] = sp[e];
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kPackThreads) rope_kernel(const uint16_t *k, const int64_t *pos, int64_t n,
+                                                            int D, Rope r, uint16_t *out) {
+  const int cpt = D / 8;
+  const int64_t total = n * cpt;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t tok = i / cpt;
+    const int ch = static_cast<int>(i % cpt);
+    const int64_t *pp = pos + tok * 3;
+    const uint4 kk = ld16(k + tok * D + ch * 8);
+    st16(out + tok * D + ch * 8, rope_chunk(kk, ch, pp[0], pp[1], pp[2], r));
+  }
+}
+
+static int make_rope(const pkv_rope_tables *t, int D, Rope &r, const char *who) {
+  if (!t->ft || !t->fy || !t->fx)
+    return fail(PKV_ERR_INVALID, "%s: the t, y and x RoPE tables must all be given", who);
+  if (t->ft_cols + t->fy_cols + t->fx_cols != D / 2)
+    return fail(PKV_ERR_INVALID, "%s: RoPE table columns %d+%d+%d != head_dim/2 = %d", who, t->ft_cols,
+                t->fy_cols, t->fx_cols, D / 2);
+  if (t->ft_rows <= 0 || t->fy_rows <= 0 || t->fx_rows <= 0)
+    return fail(PKV_ERR_INVALID, "%s: RoPE tables must have rows", who);
+  if (t->ft_cols < 0 || t->fy_cols < 0 || t->fx_cols < 0)
+    return fail(PKV_ERR_INVALID, "%s: negative RoPE table columns", who);
+  r = Rope{t->ft, t->fy, t->fx, t->ft_rows, t->ft_cols, t->fy_rows, t->fy_cols, t->fx_rows, t->fx_cols};
+  return PKV_OK;
+}
+
+}  // namespace pkv
+
+using namespace pkv;
+
+extern "C" {
+
+int pkv_plan_multi(const pkv_geometry *geo, const uint8_t *states_layer, const int64_t *valid_count_layer,
+                   const int32_t *merge_token_count_layer, const int64_t *current_t_list, int32_t num_chunks,
+                   const pkv_remap *remap, const pkv_plan_out *out, int32_t *total_tokens_out,
+                   pkv_stream_t stream) {
+  if (!geo || !states_layer || !valid_count_layer || !merge_token_count_layer || !current_t_list || !remap ||
+      !out)
+    return fail(PKV_ERR_INVALID, "mega_plan_multi: NULL argument");
+  if (num_chunks <= 0) return fail(PKV_ERR_INVALID, "mega_plan_multi: empty current_t_list");
+  if (num_chunks > kMaxPlanChunks)
+    return fail(PKV_ERR_UNSUPPORTED, "mega_plan_multi: %d chunks exceed %d", num_chunks, kMaxPlanChunks);
+  const int H = geo->num_heads;
+  if (num_chunks * H > kMaxPlanPairs)
+    return fail(PKV_ERR_UNSUPPORTED, "mega_plan_multi: %d (chunk, head) pairs exceed %d", num_chunks * H,
+                kMaxPlanPairs);
+  PlanParams p;
+  p.H = H;
+  p.S = geo->max_sink + geo->max_middle + geo->max_recent + geo->max_merge_blocks;
+  p.FSEQ = geo->frame_seqlen;
+  p.max_sink = geo->max_sink;
+  p.max_middle = geo->max_middle;
+  p.max_recent = geo->max_recent;
+  p.MMB = geo->max_merge_blocks;
+  p.C = num_chunks;
+  for (int c = 0; c < num_chunks; ++c) {
+    p.t[c] = current_t_list[c];
+    p.sync_t[c] = map_sink_time(current_t_list[c], remap->sink_mode_code, remap->sink_clamp_min,
+                                remap->sink_clamp_max, remap->decoupled_sink_lag);
+  }
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, p,
+                     reinterpret_cast<const HeadState *>(states_layer), valid_count_layer,
+                     merge_token_count_layer, *out, total_tokens_out);
+  int rc = check_launch("plan_kernel");
+  if (rc) return rc;
+  // Static bound on the packed tokens: every (chunk, head) emits at most S
+  // segments of at most max(FSEQ, MTPA) tokens.  Only when that bound can
+  // exceed the workspace is the actual total read back (one sync).
+  const int64_t seg_max = geo->frame_seqlen > geo->max_merge_tokens ? geo->frame_seqlen : geo->max_merge_tokens;
+  const int64_t bound = static_cast<int64_t>(num_chunks) * H *
+                        ((geo->max_sink + geo->max_middle + geo->max_recent) * static_cast<int64_t>(geo->frame_seqlen) +
+                         geo->max_merge_blocks * seg_max);
+  if (bound > geo->max_pack_tokens) {
+    int32_t total = 0;
+    if (hipMemcpyAsync(&total, out->cu_seqlens_k + num_chunks * H, sizeof(int32_t), hipMemcpyDeviceToHost, st) !=
+            hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+      return fail(PKV_ERR_HIP, "mega_plan_multi: readback of the packed total failed");
+    if (total > geo->max_pack_tokens)
+      return fail(PKV_ERR_CAPACITY,
+                  "mega_plan_multi: packed tokens (%d) exceed pack-workspace capacity (%lld). Either reduce "
+                  "chunks (%d) or rebuild the manager with a larger max_attend_chunks.",
+                  total, static_cast<long long>(geo->max_pack_tokens), num_chunks);
+  }
+  return PKV_OK;
+}
+
+int pkv_pack(const pkv_geometry *geo, const pkv_pools *pools, const int32_t *src_kind,
+             const int32_t *src_slot_global, const int32_t *seg_lengths, const int32_t *dst_token_offsets,
+             int32_t n_segments, const int64_t *anchor_t_remap, const pkv_rope_tables *rope,
+             pkv_stream_t stream) {
+  if (!geo || !pools) return fail(PKV_ERR_INVALID, "pyramidkv_pack: NULL geometry/pools");
+  if (n_segments == 0) return PKV_OK;
+  if (n_segments < 0 || !src_kind || !src_slot_global || !seg_lengths || !dst_token_offsets)
+    return fail(PKV_ERR_INVALID, "pyramidkv_pack: bad descriptors");
+  if (geo->head_dim % 8) return fail(PKV_ERR_INVALID, "pyramidkv_pack: head_dim must be a multiple of 8");
+  if (!pools->k_flat_out || !pools->v_flat_out) return fail(PKV_ERR_INVALID, "pyramidkv_pack: no flat outputs");
+  PackArgs a;
+  const int64_t lh = static_cast<int64_t>(geo->num_layers) * geo->num_heads;
+  a.k[0] = pools->sink_k; a.v[0] = pools->sink_v; a.pos[0] = pools->sink_pos; a.slots[0] = lh * geo->max_sink;
+  a.k[1] = pools->middle_k; a.v[1] = pools->middle_v; a.pos[1] = pools->middle_pos; a.slots[1] = lh * geo->max_middle;
+  a.k[2] = pools->recent_k; a.v[2] = pools->recent_v; a.pos[2] = pools->recent_pos; a.slots[2] = lh * geo->max_recent;
+  a.k[3] = pools->merge_k; a.v[3] = pools->merge_v; a.pos[3] = pools->merge_pos; a.slots[3] = lh * geo->max_merge_blocks;
+  a.k_out = pools->k_flat_out;
+  a.v_out = pools->v_flat_out;
+  a.pos_out = pools->pos_flat_out;
+  a.kind = src_kind;
+  a.sg = src_slot_global;
+  a.len = seg_lengths;
+  a.dst = dst_token_offsets;
+  a.tremap = anchor_t_remap;
+  a.fuse = 0;
+  if (anchor_t_remap && rope) {
+    int rc = make_rope(rope, geo->head_dim, a.rope, "pyramidkv_pack");
+    if (rc) return rc;
+    a.fuse = 1;
+  }
+  a.n_seg = n_segments;
+  a.FSEQ = geo->frame_seqlen;
+  a.MTPA = geo->max_merge_tokens;
+  a.D = geo->head_dim;
+  a.capacity = geo->max_pack_tokens;
+  const int seg_max = geo->frame_seqlen > geo->max_merge_tokens ? geo->frame_seqlen : geo->max_merge_tokens;
+  a.tiles_per_seg = (seg_max + kPackTok - 1) / kPackTok;
+  const int64_t items = static_cast<int64_t>(n_segments) * a.tiles_per_seg;
+  if (items > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "pyramidkv_pack: too many segments");
+  const int grid = static_cast<int>(items < 4096 ? items : 4096);
+  hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kPackThreads), 0, as_stream(stream), a);
+  return check_launch("pack_kernel");
+}
+
+int pkv_rope_apply(const uint16_t *k, const int64_t *pos, int64_t n_tokens, int32_t head_dim,
+                   const pkv_rope_tables *rope, uint16_t *out, pkv_stream_t stream) {
+  if (n_tokens == 0) return PKV_OK;
+  if (!k || !pos || !rope || !out || n_tokens < 0 || head_dim <= 0 || head_dim % 8)
+    return fail(PKV_ERR_INVALID, "rope_apply: bad arguments");
+  Rope r;
+  int rc = make_rope(rope, head_dim, r, "rope_apply");
+  if (rc) return rc;
+  const int64_t work = n_tokens * (head_dim / 8);
+  int64_t blocks = (work + kPackThreads - 1) / kPackThreads;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kPackThreads), 0, as_stream(stream), k,
+                     pos, n_tokens, head_dim, r, out);
+  return check_launch("rope_kernel");
+}
+
+}  // extern "C"

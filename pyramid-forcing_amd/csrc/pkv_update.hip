@@ -1,0 +1,805 @@
+// Cache-update kernels for gfx950: the per-head state machine, the
+// descriptor-driven frame copy (pyramidkv_update), the fused MegaCache.update
+// (sink/recent routing + recent FIFO shift + middle writes + positions in one
+// pass over the new chunk) and the Veil merge accumulator.
+//
+// All K/V traffic moves in 16-byte (8 x bf16) vector loads/stores; a
+// workgroup of 256 threads owns one head and a tile of tokens, so every
+// thread touches the same (token, 16-byte chunk) positions in every slot it
+// reads or writes and the in-place recent shift needs no inter-thread
+// ordering.
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "pkv_common.h"
+#include "pkv_state_machine.h"
+
+namespace pkv {
+
+// ---------------------------------------------------------------------------
+// error plumbing
+// ---------------------------------------------------------------------------
+static thread_local char g_err[512];
+
+void set_error(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int fail(int status, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PKV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return PKV_OK;
+}
+
+// ---------------------------------------------------------------------------
+// sources of new frames and of their (t, y, x) positions
+// ---------------------------------------------------------------------------
+struct FrameSrc {
+  const uint16_t *k, *v;
+  int64_t frame_stride, head_stride, tok_stride;  // elements
+  __device__ int64_t off(int f, int h, int tok) const {
+    return f * frame_stride + h * head_stride + static_cast<int64_t>(tok) * tok_stride;
+  }
+};
+
+// Either an explicit [F,H,FSEQ,3] int64 tensor, or the arithmetic grid the
+// reference builds in MegaCache.update (_mega_cache.py:203-215):
+// (t0 + f, tok / W, tok % W), identical for every head.
+struct PosSrc {
+  const int64_t *pos;
+  int64_t t0;
+  int32_t width, H, FSEQ;
+  __device__ void get(int f, int h, int tok, int64_t &t, int64_t &y, int64_t &x) const {
+    if (pos) {
+      const int64_t *p = pos + ((static_cast<int64_t>(f) * H + h) * FSEQ + tok) * 3;
+      t = p[0];
+      y = p[1];
+      x = p[2];
+    } else {
+      t = t0 + f;
+      y = tok / width;
+      x = tok % width;
+    }
+  }
+};
+
+__device__ inline uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
+
+// ---------------------------------------------------------------------------
+// mega_state_update (standalone op)
+// ---------------------------------------------------------------------------
+__global__ void state_update_kernel(HeadState *states, int H, const int64_t *t_vals, int F,
+                                    int pass_kind, pkv_state_desc out) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h < H) run_head(states, h, t_vals, F, pass_kind, out);
+}
+
+// ---------------------------------------------------------------------------
+// pyramidkv_update: descriptor-driven frame -> pool slot copy
+// (pyramidkv_update.cu:21-110).  grid = (token tiles, n_writes).
+// ---------------------------------------------------------------------------
+constexpr int kTokTile = 32;
+
+struct PoolPtrs {
+  uint16_t *k[3], *v[3];
+  int64_t *pos[3];
+  int64_t slots[3];  // L*H*max_slots of each kind, for bounds checks
+};
+
+__global__ void copy_frames_kernel(FrameSrc src, const int64_t *new_pos, PoolPtrs pools,
+                                   const int32_t *dst_kind, const int32_t *dst_slot_global,
+                                   const int32_t *src_frame, const int32_t *src_head, int H,
+                                   int FSEQ, int D, int F) {
+  const int op = blockIdx.y;
+  const int kind = dst_kind[op];
+  if (kind < 0 || kind > 2) return;
+  const int64_t sg = dst_slot_global[op];
+  const int f = src_frame[op], h = src_head[op];
+  if (sg < 0 || sg >= pools.slots[kind] || f < 0 || f >= F || h < 0 || h >= H) return;
+  const int tok0 = blockIdx.x * kTokTile;
+  const int cpt = D / 8;
+  uint16_t *dk = pools.k[kind] + sg * FSEQ * D;
+  uint16_t *dv = pools.v[kind] + sg * FSEQ * D;
+  for (int i = threadIdx.x; i < kTokTile * cpt; i += blockDim.x) {
+    const int tok = tok0 + i / cpt, c = (i % cpt) * 8;
+    if (tok >= FSEQ) break;
+    const int64_t so = src.off(f, h, tok) + c;
+    st16(dk + static_cast<int64_t>(tok) * D + c, ld16(src.k + so));
+    st16(dv + static_cast<int64_t>(tok) * D + c, ld16(src.v + so));
+  }
+  if (new_pos && pools.pos[kind]) {
+    int64_t *dp = pools.pos[kind] + sg * FSEQ * 3;
+    const int64_t *sp = new_pos + (static_cast<int64_t>(f) * H + h) * FSEQ * 3;
+    for (int i = threadIdx.x; i < kTokTile * 3; i += blockDim.x) {
+      const int tok = tok0 + i / 3;
+      if (tok >= FSEQ) break;
+      dp[static_cast<int64_t>(tok0) * 3 + i] = sp[static_cast<int64_t>(tok0) * 3 + i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fused MegaCache.update
+// ---------------------------------------------------------------------------
+// Per-head routing record produced by route_kernel and consumed by
+// scatter_kernel.
+struct Route {
+  int32_t sink_writes;   // frames 0..sink_writes-1 go to sink slots sink_first..
+  int32_t sink_first;
+  int32_t recent_first;  // frame sink_writes+i goes to recent slot recent_first+i
+  int32_t shift;         // move recent slot j+shift -> j for j < keep (0: none)
+  int32_t keep;
+  int32_t pad[3];
+};
+
+struct Workspace {
+  int32_t *desc[8];  // [H*F] each: the pkv_state_desc arrays
+  Route *route;      // [H]
+};
+
+__host__ __device__ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+__host__ __device__ inline Workspace carve_workspace(void *base, int H, int F) {
+  Workspace w;
+  char *p = static_cast<char *>(base);
+  const int64_t dbytes = align_up(static_cast<int64_t>(H) * F * 4, 256);
+  for (int i = 0; i < 8; ++i) w.desc[i] = reinterpret_cast<int32_t *>(p + i * dbytes);
+  w.route = reinterpret_cast<Route *>(p + 8 * dbytes);
+  return w;
+}
+
+// One thread per head: restore the committed counters, route the F new
+// frames between sink and recent (_mega_cache.py:226-323), advance the
+// state machine on clean passes (_mega_cache.py:329-347) and commit the
+// counters (_mega_cache.py:406-414).  The recent FIFO's shift-left is
+// applied once per block: noisy passes of a block and its clean pass all
+// restore the same committed state, shift by the same amount and overwrite
+// the same tail slots, so a pass that finds the shift already applied
+// (shift_pending) only rewrites the tail.  That reproduces the reference's
+// snapshot-and-restore contents without copying the recent pool.
+__global__ void route_kernel(HeadState *states, int H, int F, int64_t t0, int pass_kind,
+                             int shift_pending, int max_sink, int max_recent,
+                             const int64_t *sink_caps, int64_t *committed_vc, int64_t *vc,
+                             Workspace ws) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= H) return;
+  const int64_t sc = committed_vc[h * 3 + 0];
+  const int64_t mc = committed_vc[h * 3 + 1];
+  const int64_t rc = committed_vc[h * 3 + 2];
+  int64_t cap = sink_caps[h];
+  if (cap > max_sink) cap = max_sink;
+  int64_t sw = cap - sc;
+  if (sw > F) sw = F;
+  if (sw < 0) sw = 0;
+  const int64_t rw = F - sw;
+  Route r;
+  r.sink_writes = static_cast<int32_t>(sw);
+  r.sink_first = static_cast<int32_t>(sc);
+  r.shift = 0;
+  r.keep = 0;
+  int64_t rc_post = rc;
+  if (rw > 0) {
+    const int64_t total = rc + rw;
+    if (total <= max_recent) {
+      r.recent_first = static_cast<int32_t>(rc);
+      rc_post = total;
+    } else {
+      const int64_t evict = total - max_recent;
+      if (!shift_pending) {
+        r.shift = static_cast<int32_t>(evict);
+        r.keep = static_cast<int32_t>(max_recent - evict);
+      }
+      r.recent_first = static_cast<int32_t>(max_recent - rw);
+      rc_post = max_recent;
+    }
+  } else {
+    r.recent_first = static_cast<int32_t>(rc);
+  }
+  ws.route[h] = r;
+  vc[h * 3 + 0] = sc + sw;
+  vc[h * 3 + 1] = mc;
+  vc[h * 3 + 2] = rc_post;
+
+  pkv_state_desc out;
+  out.dst_kind = ws.desc[0];
+  out.dst_slot = ws.desc[1];
+  out.src_frame = ws.desc[2];
+  out.src_head = ws.desc[3];
+  out.merge_accum_slot = ws.desc[4];
+  out.merge_local_idx = ws.desc[5];
+  out.merge_finalize_completed_idx = ws.desc[6];
+  out.merge_is_new_block = ws.desc[7];
+  HeadState &s = states[h];
+  for (int f = 0; f < F; ++f) {
+    FrameDesc d = skip_desc();
+    if (pass_kind == 1) d = sm_step(s, static_cast<int32_t>(t0 + f));
+    store_desc(out, h * F + f, f, h, d);
+  }
+  if (pass_kind == 1) {
+    committed_vc[h * 3 + 0] = sc + sw;
+    committed_vc[h * 3 + 1] = mc;
+    committed_vc[h * 3 + 2] = rc_post;
+  }
+}
+
+// grid = (ceil(FSEQ / kTokTile), H).  Order per thread and (token, chunk):
+// recent shift (ascending destination slot, which never overwrites a slot
+// before it was read), then each new frame to its sink or recent slot and,
+// for middle descriptors, to its middle slot.
+__global__ void scatter_kernel(FrameSrc src, PosSrc pos, PoolPtrs pools, Workspace ws, int layer,
+                               int H, int F, int FSEQ, int D, int max_sink, int max_middle,
+                               int max_recent) {
+  const int h = blockIdx.y;
+  const Route r = ws.route[h];
+  const int tok0 = blockIdx.x * kTokTile;
+  const int cpt = D / 8;
+  const int64_t lh = static_cast<int64_t>(layer) * H + h;
+  const int64_t slot_elems = static_cast<int64_t>(FSEQ) * D;
+  uint16_t *sink_k = pools.k[0] + lh * max_sink * slot_elems;
+  uint16_t *sink_v = pools.v[0] + lh * max_sink * slot_elems;
+  uint16_t *mid_k = pools.k[1] + lh * max_middle * slot_elems;
+  uint16_t *mid_v = pools.v[1] + lh * max_middle * slot_elems;
+  uint16_t *rec_k = pools.k[2] + lh * max_recent * slot_elems;
+  uint16_t *rec_v = pools.v[2] + lh * max_recent * slot_elems;
+  const int32_t *dkind = ws.desc[0];
+  const int32_t *dslot = ws.desc[1];
+
+  for (int i = threadIdx.x; i < kTokTile * cpt; i += blockDim.x) {
+    const int tok = tok0 + i / cpt, c = (i % cpt) * 8;
+    if (tok >= FSEQ) break;
+    const int64_t e = static_cast<int64_t>(tok) * D + c;
+    for (int j = 0; j < r.keep; ++j) {
+      const uint4 kk = ld16(rec_k + (j + r.shift) * slot_elems + e);
+      const uint4 vv = ld16(rec_v + (j + r.shift) * slot_elems + e);
+      st16(rec_k + j * slot_elems + e, kk);
+      st16(rec_v + j * slot_elems + e, vv);
+    }
+    for (int f = 0; f < F; ++f) {
+      const int64_t so = src.off(f, h, tok) + c;
+      const uint4 kk = ld16(src.k + so);
+      const uint4 vv = ld16(src.v + so);
+      if (f < r.sink_writes) {
+        const int64_t s = r.sink_first + f;
+        st16(sink_k + s * slot_elems + e, kk);
+        st16(sink_v + s * slot_elems + e, vv);
+      } else {
+        const int64_t s = r.recent_first + (f - r.sink_writes);
+        st16(rec_k + s * slot_elems + e, kk);
+        st16(rec_v + s * slot_elems + e, vv);
+      }
+      if (dkind[h * F + f] == PKV_DST_MIDDLE) {
+        const int64_t s = dslot[h * F + f];
+        if (s >= 0 && s < max_middle) {
+          st16(mid_k + s * slot_elems + e, kk);
+          st16(mid_v + s * slot_elems + e, vv);
+        }
+      }
+    }
+  }
+
+  // positions: one thread per token of the tile
+  const int t = threadIdx.x;
+  if (t < kTokTile && tok0 + t < FSEQ) {
+    const int tok = tok0 + t;
+    const int64_t pe = static_cast<int64_t>(tok) * 3;
+    const int64_t pslot = static_cast<int64_t>(FSEQ) * 3;
+    int64_t *sink_p = pools.pos[0] + lh * max_sink * pslot;
+    int64_t *mid_p = pools.pos[1] + lh * max_middle * pslot;
+    int64_t *rec_p = pools.pos[2] + lh * max_recent * pslot;
+    for (int j = 0; j < r.keep; ++j) {
+      const int64_t *sp = rec_p + (j + r.shift) * pslot + pe;
+      const int64_t a = sp[0], b = sp[1], cc = sp[2];
+      int64_t *dp = rec_p + j * pslot + pe;
+      dp[0] = a;
+      dp[1] = b;
+      dp[2] = cc;
+    }
+    for (int f = 0; f < F; ++f) {
+      int64_t pt, py, px;
+      pos.get(f, h, tok, pt, py, px);
+      int64_t *dp;
+      if (f < r.sink_writes)
+        dp = sink_p + (r.sink_first + f) * pslot + pe;
+      else
+        dp = rec_p + (r.recent_first + (f - r.sink_writes)) * pslot + pe;
+      dp[0] = pt;
+      dp[1] = py;
+      dp[2] = px;
+      if (dkind[h * F + f] == PKV_DST_MIDDLE) {
+        const int64_t s = dslot[h * F + f];
+        if (s >= 0 && s < max_middle) {
+          int64_t *mp = mid_p + s * pslot + pe;
+          mp[0] = pt;
+          mp[1] = py;
+          mp[2] = px;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Veil merge accumulator (mega_merge_accum.cu:52-252)
+// ---------------------------------------------------------------------------
+// Two launches.  merge_prep_kernel (one workgroup per head, frames in order)
+// owns every piece of state shared between frames: on a new block it groups
+// the frame's tokens into patch x patch spatial groups, writes the group
+// ids, tokens-per-group, group positions and group count, and builds the
+// per-group member lists in ascending token order; for each merge frame it
+// snapshots the member lists, group count and running weight sum into a
+// per-(head, frame) workspace entry, and on finalize writes the anchor
+// positions and token count.  merge_accum_kernel (many workgroups per head)
+// then only reads those snapshots: each workgroup owns a fixed range of
+// groups of its head, zeroes them on a new block, adds the frame's tokens
+// in ascending order (one fp32 add per token, the reference's accumulation
+// sequence) and writes bf16(sum * (1 / divisor)) on finalize.
+constexpr int kGroupsPerWg = 32;
+constexpr int kMergeThreads = 256;
+constexpr int kMaxMergeFseq = 8192;
+constexpr int kMaxMergeGroups = 1024;
+
+struct MergeWs {  // one entry per (head, frame)
+  int32_t *members;  // [H*F][FSEQ]
+  int32_t *gstart;   // [H*F][MTPA+1]
+  int32_t *ng;       // [H*F]
+  float *wsum;       // [H*F]
+};
+
+__host__ __device__ inline int64_t merge_ws_bytes(int H, int F, int FSEQ, int MTPA) {
+  const int64_t n = static_cast<int64_t>(H) * F;
+  return align_up(n * FSEQ * 4, 256) + align_up(n * (MTPA + 1) * 4, 256) + 2 * align_up(n * 4, 256);
+}
+
+__host__ __device__ inline MergeWs carve_merge_ws(void *base, int H, int F, int FSEQ, int MTPA) {
+  const int64_t n = static_cast<int64_t>(H) * F;
+  char *p = static_cast<char *>(base);
+  MergeWs w;
+  w.members = reinterpret_cast<int32_t *>(p);
+  p += align_up(n * FSEQ * 4, 256);
+  w.gstart = reinterpret_cast<int32_t *>(p);
+  p += align_up(n * (MTPA + 1) * 4, 256);
+  w.ng = reinterpret_cast<int32_t *>(p);
+  p += align_up(n * 4, 256);
+  w.wsum = reinterpret_cast<float *>(p);
+  return w;
+}
+
+struct MergeArgs {
+  const HeadState *states;
+  FrameSrc src;
+  PosSrc pos;
+  const int32_t *desc_kind, *desc_slot, *desc_fin, *desc_new;
+  const float *weights;  // [F] or null
+  pkv_merge_layer ml;
+  MergeWs ws;
+  int H, F, FSEQ, D, MMA, MMB, MTPA;
+};
+
+// Stable CSR of gid[0..FSEQ) over groups [0, ng): gstart (exclusive prefix
+// of the counts) and members (tokens of each group in ascending order).
+// Wave 0 places the tokens 64 at a time; the rank of a token among equal
+// group ids of its 64-token chunk comes from a match mask built with one
+// ballot per bit of the group id.
+__device__ void build_csr(const int32_t *gid, int FSEQ, int ng, int32_t *cnt, int32_t *gstart, int32_t *members) {
+  const int tid = threadIdx.x;
+  for (int g = tid; g < ng; g += blockDim.x) cnt[g] = 0;
+  __syncthreads();
+  for (int t = tid; t < FSEQ; t += blockDim.x) atomicAdd(&cnt[gid[t]], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int32_t acc = 0;
+    for (int g = 0; g < ng; ++g) {
+      gstart[g] = acc;
+      acc += cnt[g];
+      cnt[g] = 0;  // reused as the running fill count
+    }
+    gstart[ng] = acc;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    int bits = 1;
+    while ((1 << bits) < ng) ++bits;
+    const uint64_t below = (tid == 0) ? 0ull : (~0ull >> (64 - tid));
+    for (int c0 = 0; c0 < FSEQ; c0 += 64) {
+      const int t = c0 + tid;
+      const bool valid = t < FSEQ;
+      const int g = valid ? gid[t] : -1;
+      uint64_t match = __ballot(valid);
+      for (int b = 0; b < bits; ++b) {
+        const uint64_t ones = __ballot(valid && ((g >> b) & 1));
+        match &= ((g >> b) & 1) ? ones : ~ones;
+      }
+      if (valid) {
+        const int rank = __popcll(match & below);
+        const int base = cnt[g];
+        members[gstart[g] + base + rank] = t;
+        // the highest lane of each group advances its fill count
+        if ((match >> tid) == 1ull) cnt[g] = base + __popcll(match);
+      }
+      // LDS accesses of one wave execute in program order, so the next
+      // chunk sees this chunk's count updates without a barrier
+    }
+  }
+  __syncthreads();
+}
+
+__global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) {
+  extern __shared__ int32_t smem[];
+  int32_t *gid = smem;                          // [FSEQ]
+  int32_t *members = gid + a.FSEQ;              // [FSEQ]
+  int32_t *gstart = members + a.FSEQ;           // [kMaxMergeGroups + 1]
+  int32_t *cnt = gstart + kMaxMergeGroups + 1;  // [kMaxMergeGroups]
+  __shared__ int32_t s_maxy, s_maxx;
+  const int h = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int MTPA = a.MTPA;
+  const int32_t bf = a.states[h].block_frames;
+  const int32_t patch = a.states[h].patch_size;
+
+  for (int f = 0; f < a.F; ++f) {
+    const int di = h * a.F + f;
+    const int kind = a.desc_kind[di];
+    const int slot = a.desc_slot[di];
+    if (kind != PKV_DST_MERGE_ACCUM || slot < 0 || slot >= a.MMA) continue;
+    const int is_new = a.desc_new[di];
+    const int fin = a.desc_fin[di];
+    const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
+    int32_t *gids_g = a.ml.accum_group_ids + hs * a.FSEQ;
+    int ng;
+    if (is_new) {
+      if (tid == 0) { s_maxy = -1; s_maxx = -1; }
+      __syncthreads();
+      int32_t my = -1, mx = -1;
+      for (int t = tid; t < a.FSEQ; t += blockDim.x) {
+        int64_t pt, py, px;
+        a.pos.get(f, h, t, pt, py, px);
+        const int32_t y = static_cast<int32_t>(py), x = static_cast<int32_t>(px);
+        my = y > my ? y : my;
+        mx = x > mx ? x : mx;
+      }
+      atomicMax(&s_maxy, my);
+      atomicMax(&s_maxx, mx);
+      __syncthreads();
+      const int32_t cols = (s_maxx >= 0 && patch > 0) ? (s_maxx / patch + 1) : 1;
+      const int32_t rows = (s_maxy >= 0 && patch > 0) ? (s_maxy / patch + 1) : 1;
+      ng = rows * cols;
+      if (ng > MTPA) ng = MTPA;
+      for (int t = tid; t < a.FSEQ; t += blockDim.x) {
+        int64_t pt, py, px;
+        a.pos.get(f, h, t, pt, py, px);
+        const int32_t y = static_cast<int32_t>(py), x = static_cast<int32_t>(px);
+        int32_t g = (patch > 0 ? y / patch : 0) * cols + (patch > 0 ? x / patch : 0);
+        if (g < 0 || g >= ng) g = 0;
+        gid[t] = g;
+        gids_g[t] = g;
+      }
+      int64_t tpos, ty, tx;
+      a.pos.get(f, h, 0, tpos, ty, tx);
+      for (int g = tid; g < ng; g += blockDim.x) {
+        int64_t *ap = a.ml.accum_pos + (hs * MTPA + g) * 3;
+        ap[0] = tpos;
+        ap[1] = (g / cols) * patch;
+        ap[2] = (g % cols) * patch;
+      }
+      if (tid == 0) {
+        a.ml.accum_num_groups[hs] = ng;
+        if (a.ml.accum_weight_sum) a.ml.accum_weight_sum[hs] = 0.0f;
+      }
+    } else {
+      ng = a.ml.accum_num_groups[hs];
+      if (ng > MTPA) ng = MTPA;
+      for (int t = tid; t < a.FSEQ; t += blockDim.x) gid[t] = gids_g[t];
+    }
+    __syncthreads();
+    build_csr(gid, a.FSEQ, ng, cnt, gstart, members);
+    if (is_new) {
+      float *tpg = a.ml.accum_tokens_per_group + hs * MTPA;
+      for (int g = tid; g < MTPA; g += blockDim.x)
+        tpg[g] = g < ng ? static_cast<float>(gstart[g + 1] - gstart[g]) * static_cast<float>(bf) : 0.0f;
+    }
+    // per-frame snapshot for the accumulation launch
+    int32_t *wm = a.ws.members + static_cast<int64_t>(di) * a.FSEQ;
+    int32_t *wg = a.ws.gstart + static_cast<int64_t>(di) * (MTPA + 1);
+    for (int t = tid; t < a.FSEQ; t += blockDim.x) wm[t] = members[t];
+    for (int g = tid; g <= ng; g += blockDim.x) wg[g] = gstart[g];
+    if (tid == 0) {
+      a.ws.ng[di] = ng;
+      float ws = 1.0f;
+      if (a.weights && a.ml.accum_weight_sum) {
+        ws = a.ml.accum_weight_sum[hs] + a.weights[f];
+        a.ml.accum_weight_sum[hs] = ws;
+      }
+      a.ws.wsum[di] = ws;
+    }
+    if (fin >= 0 && fin < a.MMB) {
+      const int64_t hp = static_cast<int64_t>(h) * a.MMB + fin;
+      for (int g = tid; g < ng; g += blockDim.x) {
+        const int64_t *ap = a.ml.accum_pos + (hs * MTPA + g) * 3;
+        int64_t *mp = a.ml.merge_pos + (hp * MTPA + g) * 3;
+        mp[0] = ap[0];
+        mp[1] = ap[1];
+        mp[2] = ap[2];
+      }
+      if (tid == 0) a.ml.merge_token_count[hp] = ng;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a) {
+  const int h = blockIdx.y;
+  const int g0 = blockIdx.x * kGroupsPerWg;
+  const int tid = threadIdx.x;
+  const int D = a.D, MTPA = a.MTPA;
+  const int cpt = D / 8;
+  const int32_t bf = a.states[h].block_frames;
+  for (int f = 0; f < a.F; ++f) {
+    const int di = h * a.F + f;
+    const int kind = a.desc_kind[di];
+    const int slot = a.desc_slot[di];
+    if (kind != PKV_DST_MERGE_ACCUM || slot < 0 || slot >= a.MMA) continue;
+    const int is_new = a.desc_new[di];
+    const int fin = a.desc_fin[di];
+    const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
+    float *sum_k = a.ml.accum_sum_k + hs * MTPA * D;
+    float *sum_v = a.ml.accum_sum_v + hs * MTPA * D;
+    const int32_t *members = a.ws.members + static_cast<int64_t>(di) * a.FSEQ;
+    const int32_t *gstart = a.ws.gstart + static_cast<int64_t>(di) * (MTPA + 1);
+    const int ng = a.ws.ng[di];
+    const float w = a.weights ? a.weights[f] : 1.0f;
+    // thread = (group, 8-wide dim chunk); the mapping is the same for every
+    // frame, so each accumulator element has a single owner thread
+    for (int i = tid; i < kGroupsPerWg * cpt; i += blockDim.x) {
+      const int g = g0 + i / cpt, c = (i % cpt) * 8;
+      if (g >= MTPA) break;
+      float *pk = sum_k + static_cast<int64_t>(g) * D + c;
+      float *pv = sum_v + static_cast<int64_t>(g) * D + c;
+      float ak[8], av[8];
+      if (is_new) {
+        for (int e = 0; e < 8; ++e) { ak[e] = 0.0f; av[e] = 0.0f; }
+      } else {
+        for (int e = 0; e < 8; ++e) { ak[e] = pk[e]; av[e] = pv[e]; }
+      }
+      if (g < ng) {
+        for (int m = gstart[g]; m < gstart[g + 1]; ++m) {
+          const int64_t so = a.src.off(f, h, members[m]) + c;
+          const uint4 kk = ld16(a.src.k + so);
+          const uint4 vv = ld16(a.src.v + so);
+          const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+          const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+          for (int e = 0; e < 4; ++e) {
+            const float k0 = bf16_to_f32(static_cast<uint16_t>(kw[e] & 0xffff));
+            const float k1 = bf16_to_f32(static_cast<uint16_t>(kw[e] >> 16));
+            const float v0 = bf16_to_f32(static_cast<uint16_t>(vw[e] & 0xffff));
+            const float v1 = bf16_to_f32(static_cast<uint16_t>(vw[e] >> 16));
+            if (a.weights) {
+              ak[2 * e] = __fadd_rn(ak[2 * e], __fmul_rn(w, k0));
+              ak[2 * e + 1] = __fadd_rn(ak[2 * e + 1], __fmul_rn(w, k1));
+              av[2 * e] = __fadd_rn(av[2 * e], __fmul_rn(w, v0));
+              av[2 * e + 1] = __fadd_rn(av[2 * e + 1], __fmul_rn(w, v1));
+            } else {
+              ak[2 * e] += k0;
+              ak[2 * e + 1] += k1;
+              av[2 * e] += v0;
+              av[2 * e + 1] += v1;
+            }
+          }
+        }
+      }
+      for (int e = 0; e < 8; ++e) { pk[e] = ak[e]; pv[e] = av[e]; }
+      if (fin >= 0 && fin < a.MMB && g < ng) {
+        const int32_t count = gstart[g + 1] - gstart[g];
+        const float div = a.weights ? static_cast<float>(count) * a.ws.wsum[di]
+                                    : static_cast<float>(count) * static_cast<float>(bf);
+        const float inv = div > 0.0f ? 1.0f / div : 0.0f;
+        const int64_t hp = static_cast<int64_t>(h) * a.MMB + fin;
+        uint4 ok, ov;
+        ok.x = pack_bf16x2(ak[0] * inv, ak[1] * inv);
+        ok.y = pack_bf16x2(ak[2] * inv, ak[3] * inv);
+        ok.z = pack_bf16x2(ak[4] * inv, ak[5] * inv);
+        ok.w = pack_bf16x2(ak[6] * inv, ak[7] * inv);
+        ov.x = pack_bf16x2(av[0] * inv, av[1] * inv);
+        ov.y = pack_bf16x2(av[2] * inv, av[3] * inv);
+        ov.z = pack_bf16x2(av[4] * inv, av[5] * inv);
+        ov.w = pack_bf16x2(av[6] * inv, av[7] * inv);
+        st16(a.ml.merge_k + (hp * MTPA + g) * D + c, ok);
+        st16(a.ml.merge_v + (hp * MTPA + g) * D + c, ov);
+      }
+    }
+  }
+}
+
+static int launch_merge(const MergeArgs &ma, hipStream_t st) {
+  if (ma.FSEQ > kMaxMergeFseq)
+    return fail(PKV_ERR_UNSUPPORTED, "merge_accum: frame_seqlen %d exceeds %d", ma.FSEQ, kMaxMergeFseq);
+  if (ma.MTPA > kMaxMergeGroups)
+    return fail(PKV_ERR_UNSUPPORTED, "merge_accum: %d tokens per anchor exceed %d", ma.MTPA, kMaxMergeGroups);
+  if (ma.D % 8 != 0) return fail(PKV_ERR_INVALID, "merge_accum: head_dim %d not a multiple of 8", ma.D);
+  const size_t smem = (2 * static_cast<size_t>(ma.FSEQ) + 2 * kMaxMergeGroups + 1) * sizeof(int32_t);
+  hipLaunchKernelGGL(merge_prep_kernel, dim3(ma.H), dim3(kMergeThreads), smem, st, ma);
+  int rc = check_launch("merge_prep_kernel");
+  if (rc) return rc;
+  dim3 grid((ma.MTPA + kGroupsPerWg - 1) / kGroupsPerWg, ma.H);
+  hipLaunchKernelGGL(merge_accum_kernel, grid, dim3(kMergeThreads), 0, st, ma);
+  return check_launch("merge_accum_kernel");
+}
+
+static PoolPtrs pool_ptrs(const pkv_geometry *g, const pkv_pools *p) {
+  PoolPtrs pp;
+  pp.k[0] = p->sink_k; pp.v[0] = p->sink_v; pp.pos[0] = p->sink_pos;
+  pp.k[1] = p->middle_k; pp.v[1] = p->middle_v; pp.pos[1] = p->middle_pos;
+  pp.k[2] = p->recent_k; pp.v[2] = p->recent_v; pp.pos[2] = p->recent_pos;
+  const int64_t lh = static_cast<int64_t>(g->num_layers) * g->num_heads;
+  pp.slots[0] = lh * g->max_sink;
+  pp.slots[1] = lh * g->max_middle;
+  pp.slots[2] = lh * g->max_recent;
+  return pp;
+}
+
+static int check_geometry(const pkv_geometry *g) {
+  if (!g) return fail(PKV_ERR_INVALID, "geometry is NULL");
+  if (g->num_layers <= 0 || g->num_heads <= 0 || g->head_dim <= 0 || g->frame_seqlen <= 0)
+    return fail(PKV_ERR_INVALID, "geometry: num_layers/num_heads/head_dim/frame_seqlen must be > 0");
+  if (g->head_dim % 8 != 0) return fail(PKV_ERR_INVALID, "geometry: head_dim %d must be a multiple of 8", g->head_dim);
+  if (g->max_sink < 0 || g->max_middle < 0 || g->max_recent < 0)
+    return fail(PKV_ERR_INVALID, "geometry: max_*_frames must be >= 0");
+  return PKV_OK;
+}
+
+}  // namespace pkv
+
+using namespace pkv;
+
+extern "C" {
+
+int pkv_abi_version(void) { return PKV_ABI_VERSION; }
+int64_t pkv_perhead_state_size(void) { return static_cast<int64_t>(sizeof(HeadState)); }
+const char *pkv_last_error(void) { return g_err; }
+
+int pkv_state_update(uint8_t *states, int32_t num_heads, const int64_t *new_t_vals,
+                     int32_t frames_in_block, int32_t pass_kind, const pkv_state_desc *desc,
+                     pkv_stream_t stream) {
+  if (num_heads == 0 || frames_in_block == 0) return PKV_OK;
+  if (!states || !new_t_vals || !desc || num_heads < 0 || frames_in_block < 0)
+    return fail(PKV_ERR_INVALID, "mega_state_update: bad arguments");
+  const int threads = 64;
+  hipLaunchKernelGGL(state_update_kernel, dim3((num_heads + threads - 1) / threads), dim3(threads), 0,
+                     as_stream(stream), reinterpret_cast<HeadState *>(states), num_heads, new_t_vals,
+                     frames_in_block, pass_kind, *desc);
+  return check_launch("state_update_kernel");
+}
+
+int pkv_update_frames(const pkv_geometry *geo, const pkv_pools *pools, const uint16_t *new_k,
+                      const uint16_t *new_v, const int64_t *new_pos, int32_t frames_in_block,
+                      const int32_t *dst_kind, const int32_t *dst_slot_global, const int32_t *src_frame,
+                      const int32_t *src_head, int32_t n_writes, pkv_stream_t stream) {
+  int rc = check_geometry(geo);
+  if (rc) return rc;
+  if (n_writes == 0) return PKV_OK;
+  if (!new_k || !new_v || !dst_kind || !dst_slot_global || !src_frame || !src_head || n_writes < 0)
+    return fail(PKV_ERR_INVALID, "pyramidkv_update: bad arguments");
+  const int H = geo->num_heads, FSEQ = geo->frame_seqlen, D = geo->head_dim;
+  FrameSrc src{new_k, new_v, static_cast<int64_t>(H) * FSEQ * D, static_cast<int64_t>(FSEQ) * D, D};
+  dim3 grid((FSEQ + kTokTile - 1) / kTokTile, n_writes);
+  hipLaunchKernelGGL(copy_frames_kernel, grid, dim3(256), 0, as_stream(stream), src, new_pos,
+                     pool_ptrs(geo, pools), dst_kind, dst_slot_global, src_frame, src_head, H, FSEQ, D,
+                     frames_in_block);
+  return check_launch("copy_frames_kernel");
+}
+
+int pkv_merge_accum(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t D, int32_t MMA,
+                    int32_t MMB, int32_t MTPA, const uint16_t *new_k, const uint16_t *new_v,
+                    const int64_t *new_pos, const int32_t *desc_dst_kind,
+                    const int32_t *desc_merge_accum_slot,
+                    const int32_t *desc_merge_finalize_completed_idx,
+                    const int32_t *desc_merge_is_new_block, const float *frame_weights,
+                    const pkv_merge_layer *ml, void *workspace, pkv_stream_t stream) {
+  if (H == 0 || F == 0) return PKV_OK;
+  if (!states || !new_k || !new_v || !new_pos || !ml || !workspace || H < 0 || F < 0 || FSEQ <= 0 ||
+      D <= 0 || MMA <= 0 || MMB <= 0 || MTPA <= 0)
+    return fail(PKV_ERR_INVALID, "mega_merge_accum: bad arguments");
+  if (frame_weights && !ml->accum_weight_sum)
+    return fail(PKV_ERR_INVALID, "mega_merge_accum: weighted merge needs accum_weight_sum");
+  MergeArgs ma;
+  ma.states = reinterpret_cast<const HeadState *>(states);
+  ma.src = FrameSrc{new_k, new_v, static_cast<int64_t>(H) * FSEQ * D, static_cast<int64_t>(FSEQ) * D, D};
+  ma.pos = PosSrc{new_pos, 0, 1, H, FSEQ};
+  ma.desc_kind = desc_dst_kind;
+  ma.desc_slot = desc_merge_accum_slot;
+  ma.desc_fin = desc_merge_finalize_completed_idx;
+  ma.desc_new = desc_merge_is_new_block;
+  ma.weights = frame_weights;
+  ma.ml = *ml;
+  if (!frame_weights) ma.ml.accum_weight_sum = nullptr;
+  ma.ws = carve_merge_ws(workspace, H, F, FSEQ, MTPA);
+  ma.H = H; ma.F = F; ma.FSEQ = FSEQ; ma.D = D; ma.MMA = MMA; ma.MMB = MMB; ma.MTPA = MTPA;
+  return launch_merge(ma, as_stream(stream));
+}
+
+int64_t pkv_merge_workspace_size(int32_t H, int32_t F, int32_t FSEQ, int32_t MTPA) {
+  return merge_ws_bytes(H, F, FSEQ, MTPA);
+}
+
+static int64_t update_ws_bytes(int H, int F) {
+  return 8 * align_up(static_cast<int64_t>(H) * F * 4, 256) + align_up(static_cast<int64_t>(H) * sizeof(Route), 256);
+}
+
+int64_t pkv_cache_update_workspace_size(const pkv_geometry *geo, int32_t frames) {
+  if (!geo || frames <= 0) return 0;
+  return update_ws_bytes(geo->num_heads, frames) +
+         merge_ws_bytes(geo->num_heads, frames, geo->frame_seqlen, geo->max_merge_tokens);
+}
+
+int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_update_args *a,
+                     pkv_stream_t stream) {
+  int rc = check_geometry(geo);
+  if (rc) return rc;
+  if (!pools || !a || !a->new_k || !a->new_v || !a->states_layer || !a->sink_caps_layer ||
+      !a->committed_vc_layer || !a->workspace)
+    return fail(PKV_ERR_INVALID, "cache_update: NULL argument");
+  const int H = geo->num_heads, FSEQ = geo->frame_seqlen, D = geo->head_dim;
+  if (a->layer < 0 || a->layer >= geo->num_layers) return fail(PKV_ERR_INVALID, "cache_update: layer out of range");
+  if (a->frames <= 0 || a->frames > geo->max_recent)
+    return fail(PKV_ERR_UNSUPPORTED, "cache_update: frames per block (%d) must be in [1, max_recent=%d]",
+                a->frames, geo->max_recent);
+  if (a->spatial_width <= 0) return fail(PKV_ERR_INVALID, "cache_update: spatial_width must be > 0");
+  hipStream_t st = as_stream(stream);
+  Workspace ws = carve_workspace(a->workspace, H, a->frames);
+  int64_t *vc = pools->valid_count + static_cast<int64_t>(a->layer) * H * 3;
+  hipLaunchKernelGGL(route_kernel, dim3((H + 63) / 64), dim3(64), 0, st,
+                     reinterpret_cast<HeadState *>(a->states_layer), H, a->frames, a->t0, a->pass_kind,
+                     a->shift_pending, geo->max_sink, geo->max_recent, a->sink_caps_layer,
+                     a->committed_vc_layer, vc, ws);
+  if ((rc = check_launch("route_kernel"))) return rc;
+  FrameSrc src{a->new_k, a->new_v, static_cast<int64_t>(FSEQ) * a->tok_stride, a->head_stride, a->tok_stride};
+  PosSrc pos{nullptr, a->t0, a->spatial_width, H, FSEQ};
+  dim3 grid((FSEQ + kTokTile - 1) / kTokTile, H);
+  hipLaunchKernelGGL(scatter_kernel, grid, dim3(256), 0, st, src, pos, pool_ptrs(geo, pools), ws, a->layer,
+                     H, a->frames, FSEQ, D, geo->max_sink, geo->max_middle, geo->max_recent);
+  if ((rc = check_launch("scatter_kernel"))) return rc;
+  if (a->pass_kind == 1 && a->has_merge_head) {
+    const int64_t l = a->layer;
+    const int MMA = geo->max_merge_active, MMB = geo->max_merge_blocks, MTPA = geo->max_merge_tokens;
+    MergeArgs ma;
+    ma.states = reinterpret_cast<const HeadState *>(a->states_layer);
+    ma.src = src;
+    ma.pos = pos;
+    ma.desc_kind = ws.desc[0];
+    ma.desc_slot = ws.desc[4];
+    ma.desc_fin = ws.desc[6];
+    ma.desc_new = ws.desc[7];
+    ma.weights = nullptr;
+    ma.ml.accum_sum_k = pools->merge_accum_sum_k + l * H * MMA * MTPA * D;
+    ma.ml.accum_sum_v = pools->merge_accum_sum_v + l * H * MMA * MTPA * D;
+    ma.ml.accum_pos = pools->merge_accum_pos + l * H * MMA * MTPA * 3;
+    ma.ml.accum_group_ids = pools->merge_accum_group_ids + l * H * MMA * FSEQ;
+    ma.ml.accum_tokens_per_group = pools->merge_accum_tokens_per_group + l * H * MMA * MTPA;
+    ma.ml.accum_num_groups = pools->merge_accum_num_groups + l * H * MMA;
+    ma.ml.accum_weight_sum = nullptr;
+    ma.ml.merge_k = pools->merge_k + l * H * MMB * MTPA * D;
+    ma.ml.merge_v = pools->merge_v + l * H * MMB * MTPA * D;
+    ma.ml.merge_pos = pools->merge_pos + l * H * MMB * MTPA * 3;
+    ma.ml.merge_token_count = pools->merge_token_count + l * H * MMB;
+    ma.ws = carve_merge_ws(static_cast<char *>(a->workspace) + update_ws_bytes(H, a->frames), H, a->frames, FSEQ,
+                           MTPA);
+    ma.H = H; ma.F = a->frames; ma.FSEQ = FSEQ; ma.D = D; ma.MMA = MMA; ma.MMB = MMB; ma.MTPA = MTPA;
+    if ((rc = launch_merge(ma, st))) return rc;
+  }
+  return PKV_OK;
+}
+
+}  // extern "C"
