@@ -1,0 +1,68 @@
+"""torch.ops.adahead access (reference: pyramidkv/_ops.py:16-167).
+
+Loads the in-tree torch binding (_lib/libpyramidkv_torch.so, which links
+the HIP library _lib/libpyramidkv_hip.so) and exposes the registered ops.
+If the binding is missing, ``ops()`` raises the reference's RuntimeError;
+there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+TORCH_LIB = os.path.join(_HERE, "_lib", "libpyramidkv_torch.so")
+_loaded = None
+
+
+def _ensure_loaded() -> bool:
+    global _loaded
+    if _loaded is None:
+        try:
+            torch.ops.load_library(TORCH_LIB)
+            _loaded = True
+        except (OSError, RuntimeError):
+            _loaded = False
+    return _loaded
+
+
+def available() -> bool:
+    return _ensure_loaded() and hasattr(torch.ops, "adahead")
+
+
+def ops():
+    if not _ensure_loaded():
+        raise RuntimeError("CUDA scatter extension not available")
+    return torch.ops.adahead
+
+
+_EMPTY = {}
+
+
+def _empty(dtype, device):
+    key = (dtype, str(device))
+    t = _EMPTY.get(key)
+    if t is None:
+        t = _EMPTY[key] = torch.empty(0, dtype=dtype, device=device)
+    return t
+
+
+def pyramidkv_pack(mgr, src_kind, src_slot_global, seg_lengths, dst_token_offsets, *, anchor_t_remap=None,
+                   freqs_ft_flat=None, freqs_fy_flat=None, freqs_fx_flat=None) -> None:
+    """Empty tensors stand in for omitted RoPE arguments (pure gather)."""
+    d = src_kind.device
+    e64, ef = _empty(torch.int64, d), _empty(torch.float32, d)
+    ops().pyramidkv_pack(mgr, src_kind, src_slot_global, seg_lengths, dst_token_offsets,
+                         anchor_t_remap if anchor_t_remap is not None else e64,
+                         freqs_ft_flat if freqs_ft_flat is not None else ef,
+                         freqs_fy_flat if freqs_fy_flat is not None else ef,
+                         freqs_fx_flat if freqs_fx_flat is not None else ef)
+
+
+def ragged_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_scale=None, kv_per_head=True,
+                     causal=False):
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** -0.5
+    return ops().ragged_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), float(softmax_scale),
+                                  bool(kv_per_head), bool(causal))
