@@ -1,0 +1,180 @@
+"""End-to-end parity of the pyramidkv host API on the GPU: MegaCache
+update (fused route + scatter + state machine + Veil merge), the device
+plan, pack with fused RoPE and the ragged attention, driven through
+torch.ops.adahead exactly as the causal DiT drives the reference's
+MegaCache (pyramidkv/_mega_cache.py:136-523), against the CPU model
+oracle.MegaCacheRef over multi-block rollouts with noisy and clean
+passes.  Pools, counters, state records, plans and packed K/V/pos are
+compared bit-exactly; attention within bf16 tolerance of float64."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+if torch.cuda.is_available():
+    from gpu_util import DEV, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+ATOL_MAX, ATOL_MEAN = 2e-2, 2e-3
+
+
+def _build(L, H, D, FS, W, labels, max_sink=3, max_middle=24, max_recent=4, chunks=3):
+    from pyramidkv import factory
+    from pyramidkv._mega_cache import build_mega_caches
+    from pyramidkv.rope import wan_freqs
+    comps = factory.shipped_compositions(L, H, labels=labels)
+    caches = build_mega_caches(L, H, D, FS, max_sink, max_middle, max_recent, comps, max_attend_chunks=chunks,
+                               device=DEV, freqs=wan_freqs(D), spatial_width=W, spatial_height=FS // W,
+                               **factory.PYRAMID_FORCING_REMAP)
+    ctx = caches[0].ctx
+    tables = O.rope_tables(D)
+    # the pack reads exactly the oracle's tables (their construction is pinned on the CPU)
+    ctx.freq_parts_flat = tuple(to_dev(t) for t in tables)
+    g = O.Geometry(L, H, D, FS, max_sink, max_middle, max_recent, max_attend_chunks=chunks)
+    states = to_np(ctx.states_bytes).reshape(L, -1)
+    ref = O.MegaCacheRef(g, states, to_np(ctx.sink_caps_per_head), spatial_width=W, sink_mode=1, cmin=18, cmax=21,
+                         lag=0, tables=tables)
+    return caches, ref, g
+
+
+def _compare_pools(caches, ref: O.MegaCacheRef, where: str):
+    mgr = caches[0].ctx.mgr
+    pairs = [("sink_k", mgr.sink_k_pool()), ("sink_v", mgr.sink_v_pool()), ("sink_pos", mgr.sink_pos_pool()),
+             ("middle_k", mgr.middle_k_pool()), ("middle_v", mgr.middle_v_pool()),
+             ("middle_pos", mgr.middle_pos_pool()), ("recent_k", mgr.recent_k_pool()),
+             ("recent_v", mgr.recent_v_pool()), ("recent_pos", mgr.recent_pos_pool()),
+             ("merge_k", mgr.merge_k_pool()), ("merge_v", mgr.merge_v_pool()), ("merge_pos", mgr.merge_pos_pool()),
+             ("merge_token_count", mgr.merge_token_count()), ("valid_count", mgr.valid_count())]
+    for name, t in pairs:
+        want = getattr(ref, name)
+        got = to_np(t).reshape(want.shape)
+        if not np.array_equal(got, want):
+            bad = np.argwhere(got != want)
+            raise AssertionError(f"{where}: {name} differs at {len(bad)} places, first {bad[:4].tolist()}")
+    got_states = to_np(caches[0].ctx.states_bytes).reshape(ref.states.shape)
+    assert np.array_equal(got_states, ref.states), f"{where}: state records differ"
+
+
+def _compare_attend(cache, ref: O.MegaCacheRef, layer, start, chunks, q_u16, where):
+    """Plan + pack bit-exact, attention output vs float64 on the oracle's packed K/V."""
+    FS, H, D = ref.g.frame_seqlen, ref.g.num_heads, ref.g.head_dim
+    plan = cache.plan(start, chunks)
+    want = ref.plan_pack(layer, start, chunks)
+    names = ["cu", "sk", "sg", "sl", "dst", "traw", "tremap"]
+    n_pairs = chunks * H
+    for name, t in zip(names, plan):
+        got = to_np(t)
+        w = want[name]
+        if name == "cu":
+            got, w = got[:n_pairs + 1], w[:n_pairs + 1]
+        assert np.array_equal(got, w), f"{where}: plan {name} differs"
+    cu_k = cache.pack(plan)
+    total = want["total"]
+    mgr = cache.ctx.mgr
+    assert np.array_equal(to_np(mgr.k_flat_out()).reshape(-1, D)[:total], want["k"]), f"{where}: packed K differs"
+    assert np.array_equal(to_np(mgr.v_flat_out()).reshape(-1, D)[:total], want["v"]), f"{where}: packed V differs"
+    assert np.array_equal(to_np(mgr.pos_flat_out())[:total], want["pos"]), f"{where}: packed pos differs"
+    q = to_dev(q_u16).view(torch.bfloat16).view(1, chunks * FS, H, D)
+    out = cache.attend(q, start)
+    cu_q = np.arange(0, chunks * FS + 1, FS)
+    exp = O.ragged_attention_ref(O.bf16_to_f32(q_u16).astype(np.float64), O.bf16_to_f32(want["k"]),
+                                 O.bf16_to_f32(want["v"]), cu_q, want["cu"][:n_pairs + 1], heads_q=H,
+                                 kv_per_head=True)
+    err = np.abs(out[0].float().cpu().numpy().astype(np.float64) - exp)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, f"{where}: attention max {err.max()} mean {err.mean()}"
+    del cu_k
+
+
+def _rand_bf16(rng, *shape):
+    return O.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))
+
+
+@pytest.mark.parametrize("seed,block_sizes,noisy_passes", [
+    (0, [3] * 9, 2),
+    (1, [1] + [3] * 8, 1),
+    (2, [2, 2, 3, 1, 3, 3, 2, 3, 4], 3),
+])
+def test_megacache_rollout_bit_exact(seed, block_sizes, noisy_passes):
+    rng = np.random.default_rng(seed)
+    L, H, D, FS, W = 2, 6, 128, 64, 8
+    labels = [[-1, 1, 2, -1, 1, 2], [2, -1, 1, 1, 2, -1]]
+    print(f"megacache rollout seed={seed} blocks={block_sizes} noisy={noisy_passes}", flush=True)
+    caches, ref, g = _build(L, H, D, FS, W, labels, chunks=4)
+    t0 = 0
+    for bi, F in enumerate(block_sizes):
+        start = t0 * FS
+        for p in range(noisy_passes + 1):
+            mode = "clean" if p == noisy_passes else "noisy"
+            for layer in range(L):
+                k = _rand_bf16(rng, F * FS, H, D)
+                v = _rand_bf16(rng, F * FS, H, D)
+                kd = to_dev(k).view(torch.bfloat16).view(1, F * FS, H, D)
+                vd = to_dev(v).view(torch.bfloat16).view(1, F * FS, H, D)
+                caches[layer].update(kd, vd, start, cache_update_mode=mode)
+                ref.update(layer, k, v, start, mode)
+                where = f"block {bi} (t0={t0}, F={F}) pass {p} {mode} layer {layer}"
+                if mode == "noisy" or bi % 3 == 2 or bi == len(block_sizes) - 1:
+                    q = _rand_bf16(rng, F * FS, H, D)
+                    _compare_attend(caches[layer], ref, layer, start, F, q, where)
+            torch.cuda.synchronize()
+            _compare_pools(caches, ref, f"block {bi} pass {p} {mode}")
+        t0 += F
+
+
+def test_megacache_rejects_update_of_new_block_while_noisy_pending():
+    L, H, D, FS, W = 1, 2, 64, 16, 4
+    caches, _ref, _g = _build(L, H, D, FS, W, [[-1, 1]], chunks=2)
+    k = torch.zeros(1, FS, H, D, dtype=torch.bfloat16, device=DEV)
+    caches[0].update(k, k, 0, cache_update_mode="noisy")
+    with pytest.raises(RuntimeError, match="uncommitted noisy pass"):
+        caches[0].update(k, k, FS, cache_update_mode="noisy")
+    caches[0].update(k, k, 0, cache_update_mode="clean")
+    caches[0].update(k, k, FS, cache_update_mode="noisy")
+
+
+def test_megacache_modes_other_than_noisy_clean_are_noops():
+    L, H, D, FS, W = 1, 2, 64, 16, 4
+    caches, _ref, _g = _build(L, H, D, FS, W, [[1, 2]], chunks=2)
+    k = torch.ones(1, FS, H, D, dtype=torch.bfloat16, device=DEV)
+    caches[0].update(k, k, 0, cache_update_mode="readonly")
+    assert int(caches[0].ctx.mgr.valid_count().abs().sum()) == 0
+    caches[0].update(k, k, 0, cache_update_mode="default")  # default == clean
+    assert int(caches[0].ctx.mgr.valid_count()[0, :, 0].sum()) == 2
+
+
+def test_megacache_plan_overflow_raises():
+    """More planned tokens than the pack workspace holds is an error with the
+    reference's message, not a silent truncation."""
+    L, H, D, FS, W = 1, 2, 64, 16, 4
+    caches, _ref, _g = _build(L, H, D, FS, W, [[1, 1]], max_middle=8, chunks=1)
+    k = torch.ones(1, 3 * FS, H, D, dtype=torch.bfloat16, device=DEV)
+    for b in range(8):
+        caches[0].update(k, k, 3 * b * FS, cache_update_mode="clean")
+    q = torch.ones(1, 3 * FS, H, D, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="exceed pack-workspace capacity"):
+        caches[0].attend(q, 24 * FS)
+
+
+def test_flash_attn_varlen_swap_point_matches_float64():
+    from pyramidkv._mega_attention import _flash_attn_varlen
+    rng = np.random.default_rng(7)
+    H, D = 3, 128
+    cu_q = np.array([0, 100, 164, 300], np.int32)
+    cu_k = np.array([0, 500, 501, 900], np.int32)
+    q = _rand_bf16(rng, int(cu_q[-1]), H, D)
+    k = _rand_bf16(rng, int(cu_k[-1]), H, D)
+    v = _rand_bf16(rng, int(cu_k[-1]), H, D)
+    f = _flash_attn_varlen()
+    out = f(to_dev(q).view(torch.bfloat16), to_dev(k).view(torch.bfloat16), to_dev(v).view(torch.bfloat16),
+            to_dev(cu_q), to_dev(cu_k), 136, 400, softmax_scale=None, causal=False)
+    qf, kf, vf = (O.bf16_to_f32(a).astype(np.float64) for a in (q, k, v))
+    exp = np.zeros_like(qf)
+    for b in range(3):
+        for h in range(H):
+            exp[cu_q[b]:cu_q[b + 1], h] = O.attention_ref(qf[cu_q[b]:cu_q[b + 1], h], kf[cu_k[b]:cu_k[b + 1], h],
+                                                          vf[cu_k[b]:cu_k[b + 1], h])
+    err = np.abs(out.float().cpu().numpy() - exp)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
