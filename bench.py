@@ -7,7 +7,10 @@ BASELINE workload "config 2": 30 layers x 12 heads, head_dim 128, bf16,
 {-1, 1, 2} (Wave 10 frames, Anchor 0-12 frames, Veil 6 frames; 1 frame =
 1,560 tokens; capped at 21 frames).  One step = one launch of the ragged
 attention kernel over all 360 (layer, head) sequences, inputs resident in
-HBM.  Secondary lines report the cache update + plan + pack path.
+HBM.  The "secondary" object reports config 3 (30-layer cache update +
+plan + pack at step 40, HBM GB/s) and config 4 (Veil merge accumulate,
+HBM GB/s), each with a bit-exact check against the CPU oracle and the
+oracle's own throughput as the CPU baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 Prints one JSON line.
@@ -115,12 +118,322 @@ def cpu_baseline_attention(lk, seed: int = 0, budget_s: float = 15.0):
                        f"{secs:.1f} s")
 
 
+# ---------------------------------------------------------------------------
+# config 3: 30-layer cache update + plan + pack at step 40
+# ---------------------------------------------------------------------------
+MAX_SINK, MAX_MIDDLE, MAX_RECENT, MAX_CHUNKS = 3, 24, 4, 8
+ROW = D * 2  # bytes of one bf16 K or V row
+
+
+def _restore(dst, src):
+    for d, s_ in zip(dst, src):
+        d.copy_(s_)
+
+
+def bench_cache_step(steps: int, warmup: int, seed: int = 0, step_index: int = 40):
+    """One step = for each of the 30 layers: MegaCache.update (clean pass,
+    3 new frames) then the K/V side of MegaCache.attend (device plan for the
+    3 query frames, layer offset, pack with fused 3D RoPE).  The cache is
+    prefilled by replaying step_index-1 clean chunks under the shipped
+    policy; before every timed step the per-layer state records and
+    counters are restored so each step does the same work."""
+    import numpy as np
+    import torch
+
+    from pyramidkv import factory
+    from pyramidkv._mega_cache import build_mega_caches
+    from pyramidkv.rope import wan_freqs
+
+    dev = "cuda:0"
+    F = 3
+    comps = factory.shipped_compositions(L, H)
+    caches = build_mega_caches(L, H, D, FSEQ, MAX_SINK, MAX_MIDDLE, MAX_RECENT, comps, max_attend_chunks=MAX_CHUNKS,
+                               device=dev, freqs=wan_freqs(D), spatial_width=52, spatial_height=30,
+                               **factory.PYRAMID_FORCING_REMAP)
+    ctx = caches[0].ctx
+    mgr = ctx.mgr
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    new_kv = [((torch.randn(1, F * FSEQ, H, D, generator=g, device=dev)).to(torch.bfloat16),
+               (torch.randn(1, F * FSEQ, H, D, generator=g, device=dev)).to(torch.bfloat16)) for _ in range(L)]
+    for c in range(step_index - 1):
+        for l in range(L):
+            caches[l].update(*new_kv[l], c * F * FSEQ, cache_update_mode="clean")
+    start = (step_index - 1) * F * FSEQ
+    snap_src = [ctx.states_bytes, mgr.valid_count(), ctx.committed_vc]
+    snap = [t.clone() for t in snap_src]
+
+    def step():
+        for l in range(L):
+            caches[l].update(*new_kv[l], start, cache_update_mode="clean")
+            caches[l].attend_kv(start, F)
+
+    # algorithmic bytes of one step (from the descriptors and plans of a real step)
+    _restore(snap_src, snap)
+    packed = []
+    upd_bytes = 0
+    n_new = F * H * FSEQ  # tokens of one layer's new chunk
+    for l in range(L):
+        caches[l].update(*new_kv[l], start, cache_update_mode="clean")
+        desc = [d.cpu().numpy() for d in caches[l].last_update_descriptors(F)]
+        cu = caches[l].attend_kv(start, F)
+        packed.append(int(cu[-1].item()))
+        kind = desc[0]
+        mid = int((kind == 1).sum())
+        mrg = int((kind == 5).sum())
+        fin = int((desc[6] >= 0).sum())
+        upd_bytes += n_new * 2 * ROW  # read new K and V once
+        upd_bytes += n_new * (2 * ROW + 24)  # write the routed sink/recent destination (K, V, pos)
+        upd_bytes += mid * FSEQ * (2 * ROW + 24)  # middle-pool writes
+        upd_bytes += mrg * 390 * D * 4 * 2 * 2  # fp32 group accumulators, read + write, K and V
+        upd_bytes += fin * 390 * (2 * ROW + 24)  # finalized merge anchors
+    pack_tok = sum(packed)
+    pack_bytes = pack_tok * (2 * ROW + 2 * ROW + 48)
+    total_bytes = upd_bytes + pack_bytes
+
+    def timed(fn, n):
+        ms = []
+        for _ in range(n):
+            _restore(snap_src, snap)
+            s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s_.record()
+            fn()
+            e_.record()
+            torch.cuda.synchronize()
+            ms.append(s_.elapsed_time(e_))
+        return ms
+
+    for _ in range(max(1, warmup)):
+        _restore(snap_src, snap)
+        step()
+    torch.cuda.synchronize()
+    eager_ms = timed(step, steps)
+    # the same step captured once as a HIP graph and replayed
+    graph_ms = None
+    try:
+        _restore(snap_src, snap)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        _restore(snap_src, snap)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        for _ in range(max(1, warmup)):
+            _restore(snap_src, snap)
+            graph.replay()
+        graph_ms = timed(graph.replay, steps)
+    except Exception as exc:  # reported, not hidden
+        graph_ms = None
+        graph_err = f"{type(exc).__name__}: {exc}"[:200]
+    else:
+        graph_err = None
+    # per-launch pack time (the dominant kernel) on layer 0's plan: events on the launch stream
+    _restore(snap_src, snap)
+    step()
+    pk = []
+    for _ in range(max(3, steps)):
+        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_.record()
+        caches[0].attend_kv(start, F)
+        e_.record()
+        torch.cuda.synchronize()
+        pk.append(s_.elapsed_time(e_))
+    plan_pack_ms_l0 = float(np.median(pk))
+    return dict(caches=caches, ctx=ctx, start=start, F=F, packed=packed, pack_tok=pack_tok, pack_bytes=pack_bytes,
+                upd_bytes=upd_bytes, total_bytes=total_bytes, eager_ms=float(np.median(eager_ms)),
+                graph_ms=(float(np.median(graph_ms)) if graph_ms else None), graph_err=graph_err,
+                plan_pack_ms_l0=plan_pack_ms_l0, snap_src=snap_src, snap=snap)
+
+
+def cache_step_parity_and_cpu(r, budget_s: float = 10.0):
+    """Layer 0 of the measured step on the oracle (C restatement of
+    mega_plan_multi + pyramidkv_pack with RoPE): bit-exact comparison of the
+    packed K/V/pos and cu_seqlens_k with the device result, and the oracle's
+    plan + pack throughput on the host as the CPU baseline."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    caches, ctx, start, F = r["caches"], r["ctx"], r["start"], r["F"]
+    mgr = ctx.mgr
+    cu = caches[0].attend_kv(start, F)
+    torch.cuda.synchronize()
+
+    def host(t):
+        t = t.detach().contiguous().cpu()
+        return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+    total = int(cu[-1].item())
+    got = dict(cu=host(cu), k=host(mgr.k_flat_out()).reshape(-1, D)[:total],
+               v=host(mgr.v_flat_out()).reshape(-1, D)[:total], pos=host(mgr.pos_flat_out())[:total])
+    pools = {}
+    for name, t in (("sink", mgr.sink_k_pool()), ("middle", mgr.middle_k_pool()), ("recent", mgr.recent_k_pool()),
+                    ("merge", mgr.merge_k_pool())):
+        pools[name + "_k"] = host(t[0])
+    for name, t in (("sink", mgr.sink_v_pool()), ("middle", mgr.middle_v_pool()), ("recent", mgr.recent_v_pool()),
+                    ("merge", mgr.merge_v_pool())):
+        pools[name + "_v"] = host(t[0])
+    for name, t in (("sink", mgr.sink_pos_pool()), ("middle", mgr.middle_pos_pool()),
+                    ("recent", mgr.recent_pos_pool()), ("merge", mgr.merge_pos_pool())):
+        pools[name + "_pos"] = host(t[0])
+    g = O.Geometry(1, H, D, FSEQ, MAX_SINK, MAX_MIDDLE, MAX_RECENT, max_attend_chunks=MAX_CHUNKS)
+    states = host(ctx.states_bytes[0])
+    vc = host(mgr.valid_count()[0])
+    mtc = host(mgr.merge_token_count()[0])
+    tables = O.rope_tables(D)
+    t_list = [start // FSEQ + c for c in range(F)]
+    rm = factory_remap()
+    n = 0
+    secs = 0.0
+    ok = None
+    while n < 1 or (secs < budget_s and n < 50):
+        t0 = time.perf_counter()
+        pcu, sk, sg, sl, dst, _tr, trm, tot = O.plan_multi(g, states, vc, mtc, t_list, *rm)
+        k, v, p = O.pack(pools, g, sk, sg, sl, dst, trm, tables, capacity=tot)
+        secs += time.perf_counter() - t0
+        n += 1
+        if ok is None:
+            ok = (tot == total and np.array_equal(pcu, got["cu"]) and np.array_equal(k, got["k"])
+                  and np.array_equal(v, got["v"]) and np.array_equal(p, got["pos"]))
+    bytes_one = total * (2 * ROW + 2 * ROW + 48)
+    return ok, dict(value=round(bytes_one * n / secs / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                    sample=f"layer 0 of the step-40 plan + pack ({total} packed tokens, RoPE fused) by the oracle's "
+                           f"C restatement, {n} repetitions in {secs:.1f} s, single thread")
+
+
+def factory_remap():
+    from pyramidkv import factory
+    r = factory.PYRAMID_FORCING_REMAP
+    mode = {"lag": 0, "window_clamp": 1}[r["sink_time_mapping_mode"]]
+    return (mode, r["sink_time_clamp_min"], r["sink_time_clamp_max"], r["decoupled_sink_time_lag"])
+
+
+# ---------------------------------------------------------------------------
+# config 4: Veil merge accumulate, 40 consecutive evictions, weighted mean
+# ---------------------------------------------------------------------------
+EVICTIONS, MERGE_GROUPS = 40, 390
+
+
+def bench_merge(steps: int, warmup: int, seed: int = 0):
+    """One step = 40 consecutive evictions of one 1,560-token frame per head
+    (12 heads) into Veil merge state (patch 2, 6 completed anchors): per
+    eviction the state update (clean pass) and the weighted merge
+    accumulate, replayed as one captured HIP graph."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+    from pyramidkv import _ops
+
+    ops = _ops.ops()
+    dev = "cuda:0"
+    rng = np.random.default_rng(seed)
+    MMA, MMB, MT = 2, 6, 420
+    states0 = O.states_to_bytes([O.make_merge(2, 6) for _ in range(H)]).view(np.uint8).reshape(-1)
+    k_np = O.f32_to_bf16(rng.standard_normal((EVICTIONS, 1, H, FSEQ, D)).astype(np.float32))
+    v_np = O.f32_to_bf16(rng.standard_normal((EVICTIONS, 1, H, FSEQ, D)).astype(np.float32))
+    w_np = rng.uniform(0.1, 1.0, size=EVICTIONS).astype(np.float32)
+    pos_np = np.zeros((EVICTIONS, 1, H, FSEQ, 3), np.int64)
+    tok = np.arange(FSEQ)
+    for e in range(EVICTIONS):
+        pos_np[e, 0, :, :, 0] = e + 1
+        pos_np[e, 0, :, :, 1] = tok // 52
+        pos_np[e, 0, :, :, 2] = tok % 52
+    bf = lambda a: torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)
+    nk, nv = bf(k_np), bf(v_np)
+    npos = torch.from_numpy(pos_np).to(dev)
+    w = torch.from_numpy(w_np).to(dev)
+    tv = [torch.tensor([e + 1], dtype=torch.int64, device=dev) for e in range(EVICTIONS)]
+    states = torch.from_numpy(states0.copy()).to(dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    acc = dict(sum_k=torch.zeros(H, MMA, MT, D, **f32), sum_v=torch.zeros(H, MMA, MT, D, **f32),
+               pos=torch.zeros(H, MMA, MT, 3, dtype=torch.int64, device=dev),
+               gid=torch.zeros(H, MMA, FSEQ, dtype=torch.int32, device=dev), tpg=torch.zeros(H, MMA, MT, **f32),
+               ng=torch.zeros(H, MMA, dtype=torch.int32, device=dev), wsum=torch.zeros(H, MMA, **f32),
+               mk=torch.zeros(H, MMB, MT, D, dtype=torch.bfloat16, device=dev),
+               mv=torch.zeros(H, MMB, MT, D, dtype=torch.bfloat16, device=dev),
+               mpos=torch.zeros(H, MMB, MT, 3, dtype=torch.int64, device=dev),
+               mtc=torch.zeros(H, MMB, dtype=torch.int32, device=dev))
+    desc = [torch.full((H,), -1, dtype=torch.int32, device=dev) for _ in range(8)]
+    init = {n_: t.clone() for n_, t in acc.items()}
+
+    def reset():
+        states.copy_(torch.from_numpy(states0).to(dev))
+        for n_, t in acc.items():
+            t.copy_(init[n_])
+
+    def step():
+        for e in range(EVICTIONS):
+            ops.mega_state_update(states, tv[e], *desc, H, 1, 1)
+            ops.mega_merge_accum_weighted(states, nk[e], nv[e], npos[e], desc[0], desc[4], desc[6], desc[7],
+                                          w[e:e + 1], acc["sum_k"], acc["sum_v"], acc["pos"], acc["gid"], acc["tpg"],
+                                          acc["ng"], acc["wsum"], acc["mk"], acc["mv"], acc["mpos"], acc["mtc"])
+
+    reset()
+    step()
+    torch.cuda.synchronize()
+    got = {n_: t.cpu() for n_, t in acc.items() if n_ in ("mk", "mv", "mpos", "mtc")}
+    reset()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    reset()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    ms = []
+    for i in range(max(1, warmup) + steps):
+        reset()
+        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_.record()
+        graph.replay()
+        e_.record()
+        torch.cuda.synchronize()
+        if i >= max(1, warmup):
+            ms.append(s_.elapsed_time(e_))
+    replay_got = {n_: t.cpu() for n_, t in acc.items() if n_ in ("mk", "mv", "mpos", "mtc")}
+    graph_same = all(torch.equal(got[n_], replay_got[n_]) for n_ in got)
+    fin = EVICTIONS // 4
+    per_ev = 2 * H * FSEQ * ROW + 2 * 2 * H * MERGE_GROUPS * D * 4
+    bytes_step = EVICTIONS * per_ev + fin * H * MERGE_GROUPS * (2 * ROW + 24)
+    # oracle: the same 40 evictions on the host (bit-exact check + CPU baseline)
+    st = states0.copy()
+    z = lambda *s_, dt=np.float32: np.zeros(s_, dt)
+    oacc = dict(sum_k=z(H, MMA, MT, D), sum_v=z(H, MMA, MT, D), pos=z(H, MMA, MT, 3, dt=np.int64),
+                gid=z(H, MMA, FSEQ, dt=np.int32), tpg=z(H, MMA, MT), ng=z(H, MMA, dt=np.int32), wsum=z(H, MMA),
+                mk=z(H, MMB, MT, D, dt=np.uint16), mv=z(H, MMB, MT, D, dt=np.uint16),
+                mpos=z(H, MMB, MT, 3, dt=np.int64), mtc=z(H, MMB, dt=np.int32))
+    t0 = time.perf_counter()
+    for e in range(EVICTIONS):
+        d_ = O.state_update(st, [e + 1], 1)
+        O.merge_accum(st, k_np[e], v_np[e], pos_np[e], d_, oacc, weights=w_np[e:e + 1])
+    cpu_s = time.perf_counter() - t0
+    to_u16 = lambda t: t.view(torch.int16).numpy().view(np.uint16)
+    parity = (np.array_equal(to_u16(got["mk"]), oacc["mk"]) and np.array_equal(to_u16(got["mv"]), oacc["mv"])
+              and np.array_equal(got["mpos"].numpy(), oacc["mpos"]) and np.array_equal(got["mtc"].numpy(), oacc["mtc"]))
+    return dict(ms=float(np.median(ms)), bytes=bytes_step, parity=bool(parity), graph_same=bool(graph_same),
+                cpu=dict(value=round(bytes_step / cpu_s / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                         sample=f"the same 40 evictions (state update + weighted merge accumulate, 12 heads) by the "
+                                f"oracle's C restatement, {cpu_s:.2f} s, single thread"))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true", help="skip the config-3 / config-4 measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the pyramid-cache path needs no exchange between GPUs and this build "
@@ -153,7 +466,44 @@ def main():
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_attention(r["lk"])
+    del r
+    torch.cuda.empty_cache()
+    if not args.headline_only:
+        line["secondary"] = secondary(args)
     print(json.dumps(line))
+
+
+def secondary(args):
+    import torch
+    out = {}
+    c3 = bench_cache_step(args.steps, args.warmup)
+    ms = c3["graph_ms"] if c3["graph_ms"] is not None else c3["eager_ms"]
+    gbs = c3["total_bytes"] / (ms * 1e-3) / 1e9
+    l0_bytes = c3["packed"][0] * (2 * ROW + 2 * ROW + 48)
+    pk_gbs = l0_bytes / (c3["plan_pack_ms_l0"] * 1e-3) / 1e9
+    ok, cpu = cache_step_parity_and_cpu(c3) if not args.no_cpu_baseline else (None, None)
+    out["config3_cache_update_plan_pack"] = {
+        "value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(ms, 4),
+        "timing": "hip_graph_replay" if c3["graph_ms"] is not None else "eager",
+        "eager_ms_per_step": round(c3["eager_ms"], 4), "graph_error": c3["graph_err"],
+        "bytes_per_step": c3["total_bytes"], "update_bytes": c3["upd_bytes"], "pack_bytes": c3["pack_bytes"],
+        "packed_tokens": c3["pack_tok"], "layers": L, "heads": H, "step": 40, "policy": "shipped best_labels.csv",
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "plan_pack_layer0": {"ms": round(c3["plan_pack_ms_l0"], 4), "GB/s": round(pk_gbs, 2),
+                             "frac": round(pk_gbs / PEAK_HBM_GBS, 4)},
+        "parity_layer0_bit_exact": ok, "cpu_baseline": cpu}
+    del c3
+    torch.cuda.empty_cache()
+    c4 = bench_merge(args.steps, args.warmup)
+    gbs4 = c4["bytes"] / (c4["ms"] * 1e-3) / 1e9
+    out["config4_veil_merge"] = {
+        "value": round(gbs4, 2), "unit": "GB/s", "ms_per_step": round(c4["ms"], 4), "timing": "hip_graph_replay",
+        "evictions_per_step": EVICTIONS, "bytes_per_step": c4["bytes"],
+        "roofline": {"bound": "hbm", "achieved": round(gbs4, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs4 / PEAK_HBM_GBS, 4), "traffic": None},
+        "parity_bit_exact": c4["parity"], "graph_replay_matches_eager": c4["graph_same"], "cpu_baseline": c4["cpu"]}
+    return out
 
 
 if __name__ == "__main__":

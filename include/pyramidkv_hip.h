@@ -23,6 +23,7 @@
  *   pkv_merge_accum          mega_merge_accum.cu:268-340    (launch_mega_merge_accum)
  *   pkv_plan_multi           mega_plan.cc:286-407, 513-654  (mega_plan / mega_plan_multi)
  *   pkv_pack                 pyramidkv_pack.cu:189-311      (launch_pyramidkv_pack)
+ *   pkv_plan_pack            _mega_cache.py:461-523 (plan -> layer offset -> pack of attend)
  *   pkv_rope_apply           rope.py:18-68, triton_rope.py:17-247 (apply_rope_to_flat_k)
  *   pkv_ragged_attn_fwd      _mega_cache.py:540-559, flash_attn_varlen_func (flash-attn 2.8.3)
  *   pkv_cache_update         _mega_cache.py:136-414 (MegaCache.update: sink/recent routing,
@@ -202,6 +203,21 @@ int pkv_pack(const pkv_geometry *geo, const pkv_pools *pools,
              const int32_t *seg_lengths, const int32_t *dst_token_offsets,
              int32_t n_segments, const int64_t *anchor_t_remap,
              const pkv_rope_tables *rope, pkv_stream_t stream);
+
+/* MegaCache.attend's K/V side in two launches and no host sync: the
+ * device plan of mega_plan_multi for layer `layer` with the per-kind layer
+ * offset of _layer_offset_slot_global folded into src_slot_global
+ * (mega_plan.cc:513-654, _mega_attention.py:349-385), then pyramidkv_pack
+ * with fused RoPE (rope may be NULL: pure gather) into pools->k/v/pos_flat_out
+ * (pyramidkv_pack.cu:189-311; caller _mega_cache.py:461-523).  plan_ws holds
+ * caller-owned device buffers of C*H+1 / C*H*S entries; cu_seqlens_k
+ * receives the per-(chunk, head) offsets the attention reads.  Same
+ * capacity check and error text as pkv_plan_multi. */
+int pkv_plan_pack(const pkv_geometry *geo, const pkv_pools *pools,
+                  const uint8_t *states_layer, int32_t layer,
+                  const int64_t *current_t_list, int32_t num_chunks,
+                  const pkv_remap *remap, const pkv_rope_tables *rope,
+                  const pkv_plan_out *plan_ws, pkv_stream_t stream);
 
 /* apply_rope_to_flat_k: out[n, D] = rot(k[n, D], pos[n, 3]); out may equal k. */
 int pkv_rope_apply(const uint16_t *k, const int64_t *pos, int64_t n_tokens,

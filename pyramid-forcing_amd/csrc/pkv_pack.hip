@@ -36,6 +36,7 @@ constexpr int kMaxPlanPairs = 4096;
 
 struct PlanParams {
   int H, S, FSEQ, max_sink, max_middle, max_recent, MMB, C;
+  int32_t slot_off[4];  // per-kind layer offset added to src_slot_global (0 for the reference op)
   int64_t t[kMaxPlanChunks];
   int64_t sync_t[kMaxPlanChunks];
 };
@@ -65,9 +66,9 @@ __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int6
   };
   const int n_sink_raw = static_cast<int>(vc_h[0]);
   const int n_sink = (thresh > 0 && thresh < n_sink_raw) ? thresh : n_sink_raw;
-  for (int q = 0; q < n_sink && q < p.max_sink; ++q) put(PKV_SEG_SINK, h * p.max_sink + q, p.FSEQ, q, sync_t);
+  for (int q = 0; q < n_sink && q < p.max_sink; ++q) put(PKV_SEG_SINK, p.slot_off[0] + h * p.max_sink + q, p.FSEQ, q, sync_t);
   const int n_recent = static_cast<int>(vc_h[2]);
-  for (int r = 0; r < n_recent && r < p.max_recent; ++r) put(PKV_SEG_RECENT, h * p.max_recent + r, p.FSEQ, -1, -1);
+  for (int r = 0; r < n_recent && r < p.max_recent; ++r) put(PKV_SEG_RECENT, p.slot_off[2] + h * p.max_recent + r, p.FSEQ, -1, -1);
   if (s.kind == SK_CYCLIC) {
     const int period = s.period > 0 ? s.period : 1;
     const int bucket_cap = s.bucket_cap > 0 ? s.bucket_cap : 1;
@@ -78,7 +79,7 @@ __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int6
       if (s.cyclic_slot[i] < 0) continue;
       if (s.cyclic_t[i] < thresh) continue;
       if (s.cyclic_t[i] >= recent_min_t) continue;
-      put(PKV_SEG_MIDDLE, h * p.max_middle + i, p.FSEQ, s.cyclic_t[i], sync_t);
+      put(PKV_SEG_MIDDLE, p.slot_off[1] + h * p.max_middle + i, p.FSEQ, s.cyclic_t[i], sync_t);
       if (fp >= S) break;
     }
   } else if (s.kind == SK_STRIDE || s.kind == SK_LAG) {
@@ -86,7 +87,7 @@ __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int6
     for (int i = 0; i < tc && i < kMaxTKeyed; ++i) {
       if (s.tkey_t[i] < thresh) continue;
       if (s.tkey_t[i] >= recent_min_t) continue;
-      put(PKV_SEG_MIDDLE, h * p.max_middle + i, p.FSEQ, s.tkey_t[i], s.kind == SK_STRIDE ? sync_t : -1);
+      put(PKV_SEG_MIDDLE, p.slot_off[1] + h * p.max_middle + i, p.FSEQ, s.tkey_t[i], s.kind == SK_STRIDE ? sync_t : -1);
       if (fp >= S) break;
     }
   }
@@ -100,7 +101,7 @@ __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int6
       const int32_t tok = mtc_h[slot];
       if (tok <= 0) continue;
       if (fp >= S) break;
-      put(PKV_SEG_MERGE, h * p.MMB + slot, tok, 0, s.merge_completed_median_t[i]);
+      put(PKV_SEG_MERGE, p.slot_off[3] + h * p.MMB + slot, tok, 0, s.merge_completed_median_t[i]);
     }
   }
   for (int i = fp; i < S; ++i) {
@@ -306,12 +307,13 @@ static int make_rope(const pkv_rope_tables *t, int D, Rope &r, const char *who) 
 
 using namespace pkv;
 
-extern "C" {
-
-int pkv_plan_multi(const pkv_geometry *geo, const uint8_t *states_layer, const int64_t *valid_count_layer,
-                   const int32_t *merge_token_count_layer, const int64_t *current_t_list, int32_t num_chunks,
-                   const pkv_remap *remap, const pkv_plan_out *out, int32_t *total_tokens_out,
-                   pkv_stream_t stream) {
+// Plan launch shared by mega_plan_multi (slot_layer < 0: per-layer slot ids,
+// the reference op's output) and the fused plan + pack (slot ids offset to
+// layer slot_layer of the [L, H, slots] pools).
+static int plan_launch(const pkv_geometry *geo, const uint8_t *states_layer, const int64_t *valid_count_layer,
+                       const int32_t *merge_token_count_layer, const int64_t *current_t_list, int32_t num_chunks,
+                       const pkv_remap *remap, const pkv_plan_out *out, int32_t *total_tokens_out, int slot_layer,
+                       hipStream_t st) {
   if (!geo || !states_layer || !valid_count_layer || !merge_token_count_layer || !current_t_list || !remap ||
       !out)
     return fail(PKV_ERR_INVALID, "mega_plan_multi: NULL argument");
@@ -331,12 +333,16 @@ int pkv_plan_multi(const pkv_geometry *geo, const uint8_t *states_layer, const i
   p.max_recent = geo->max_recent;
   p.MMB = geo->max_merge_blocks;
   p.C = num_chunks;
+  const int32_t lay = slot_layer > 0 ? slot_layer : 0;
+  p.slot_off[0] = lay * H * geo->max_sink;
+  p.slot_off[1] = lay * H * geo->max_middle;
+  p.slot_off[2] = lay * H * geo->max_recent;
+  p.slot_off[3] = lay * H * geo->max_merge_blocks;
   for (int c = 0; c < num_chunks; ++c) {
     p.t[c] = current_t_list[c];
     p.sync_t[c] = map_sink_time(current_t_list[c], remap->sink_mode_code, remap->sink_clamp_min,
                                 remap->sink_clamp_max, remap->decoupled_sink_lag);
   }
-  hipStream_t st = as_stream(stream);
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, p,
                      reinterpret_cast<const HeadState *>(states_layer), valid_count_layer,
                      merge_token_count_layer, *out, total_tokens_out);
@@ -362,6 +368,16 @@ int pkv_plan_multi(const pkv_geometry *geo, const uint8_t *states_layer, const i
                   total, static_cast<long long>(geo->max_pack_tokens), num_chunks);
   }
   return PKV_OK;
+}
+
+extern "C" {
+
+int pkv_plan_multi(const pkv_geometry *geo, const uint8_t *states_layer, const int64_t *valid_count_layer,
+                   const int32_t *merge_token_count_layer, const int64_t *current_t_list, int32_t num_chunks,
+                   const pkv_remap *remap, const pkv_plan_out *out, int32_t *total_tokens_out,
+                   pkv_stream_t stream) {
+  return plan_launch(geo, states_layer, valid_count_layer, merge_token_count_layer, current_t_list, num_chunks,
+                     remap, out, total_tokens_out, -1, as_stream(stream));
 }
 
 int pkv_pack(const pkv_geometry *geo, const pkv_pools *pools, const int32_t *src_kind,
@@ -406,6 +422,24 @@ int pkv_pack(const pkv_geometry *geo, const pkv_pools *pools, const int32_t *src
   const int grid = static_cast<int>(items < 4096 ? items : 4096);
   hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kPackThreads), 0, as_stream(stream), a);
   return check_launch("pack_kernel");
+}
+
+int pkv_plan_pack(const pkv_geometry *geo, const pkv_pools *pools, const uint8_t *states_layer, int32_t layer,
+                  const int64_t *current_t_list, int32_t num_chunks, const pkv_remap *remap,
+                  const pkv_rope_tables *rope, const pkv_plan_out *plan_ws, pkv_stream_t stream) {
+  if (!geo || !pools || !plan_ws || !pools->valid_count || !pools->merge_token_count)
+    return fail(PKV_ERR_INVALID, "plan_pack: NULL argument");
+  if (layer < 0 || layer >= geo->num_layers) return fail(PKV_ERR_INVALID, "plan_pack: layer out of range");
+  const int H = geo->num_heads;
+  const int S = geo->max_sink + geo->max_middle + geo->max_recent + geo->max_merge_blocks;
+  hipStream_t st = as_stream(stream);
+  int rc = plan_launch(geo, states_layer, pools->valid_count + static_cast<int64_t>(layer) * H * 3,
+                       pools->merge_token_count + static_cast<int64_t>(layer) * H * geo->max_merge_blocks,
+                       current_t_list, num_chunks, remap, plan_ws, nullptr, layer, st);
+  if (rc) return rc;
+  return pkv_pack(geo, pools, plan_ws->src_kind, plan_ws->src_slot_global, plan_ws->seg_lengths,
+                  plan_ws->dst_token_offsets, num_chunks * H * S, rope ? plan_ws->anchor_t_remap : nullptr, rope,
+                  stream);
 }
 
 int pkv_rope_apply(const uint16_t *k, const int64_t *pos, int64_t n_tokens, int32_t head_dim,

@@ -239,6 +239,25 @@ class PyramidKVCacheManager : public torch::CustomClassHolder {
     return ws_;
   }
 
+  // Plan buffers of the fused plan + pack, sized for max_attend_chunks;
+  // cu_seqlens_k is the manager's own cu tensor.
+  pkv_plan_out plan_workspace() {
+    if (!pw_kind_.defined()) {
+      const int64_t n = mac_ * H_ * (max_total() + kMaxMergeBlocks);
+      auto o32 = at::TensorOptions().dtype(at::kInt).device(valid_count_.device());
+      auto o64 = at::TensorOptions().dtype(at::kLong).device(valid_count_.device());
+      pw_kind_ = at::empty({n}, o32);
+      pw_sg_ = at::empty({n}, o32);
+      pw_len_ = at::empty({n}, o32);
+      pw_dst_ = at::empty({n}, o32);
+      pw_traw_ = at::empty({n}, o64);
+      pw_tremap_ = at::empty({n}, o64);
+    }
+    return pkv_plan_out{cu_.data_ptr<int32_t>(), pw_kind_.data_ptr<int32_t>(), pw_sg_.data_ptr<int32_t>(),
+                        pw_len_.data_ptr<int32_t>(), pw_dst_.data_ptr<int32_t>(), pw_traw_.data_ptr<int64_t>(),
+                        pw_tremap_.data_ptr<int64_t>()};
+  }
+
   std::vector<Tensor> update_descriptors(int64_t frames) {
     Tensor ws = update_workspace(frames);
     const int64_t n = H_ * frames;
@@ -258,6 +277,7 @@ class PyramidKVCacheManager : public torch::CustomClassHolder {
   Tensor acc_k_, acc_v_, acc_pos_, acc_gid_, acc_tpg_, acc_ng_, acc_wsum_;
   Tensor ws_;
   int64_t ws_frames_ = -1;
+  Tensor pw_kind_, pw_sg_, pw_len_, pw_dst_, pw_traw_, pw_tremap_;
 };
 
 using Mgr = c10::intrusive_ptr<PyramidKVCacheManager>;
@@ -631,6 +651,41 @@ static void cache_update(Mgr mgr, Tensor states_layer, Tensor sink_caps_layer, T
 
 static std::vector<Tensor> update_descriptors(Mgr mgr, int64_t frames) { return mgr->update_descriptors(frames); }
 
+// MegaCache.attend's K/V side (pkv_plan_pack): plan for the chunks of
+// current_t_list with layer offsets folded in, then pack (+RoPE when the
+// three tables are non-empty) into the manager's flat outputs.  Returns the
+// manager's cu_seqlens_k narrowed to C*H+1 entries.
+static Tensor mega_attend_kv(Mgr mgr, Tensor states_layer, int64_t layer_idx, Tensor current_t_list,
+                             int64_t sink_mode_code, int64_t sink_clamp_min, int64_t sink_clamp_max,
+                             int64_t decoupled_sink_lag, Tensor freqs_ft_flat, Tensor freqs_fy_flat,
+                             Tensor freqs_fx_flat) {
+  TORCH_CHECK(mgr.get() != nullptr, "mega_attend_kv: manager is null");
+  mgr->require_bf16("mega_attend_kv");
+  TORCH_CHECK(states_layer.dtype() == at::kByte && states_layer.is_contiguous() &&
+                  states_layer.device() == mgr->valid_count().device() &&
+                  states_layer.numel() >= mgr->num_heads() * pkv_perhead_state_size(),
+              "mega_attend_kv: states_layer must be a contiguous uint8 [H * 600] tensor on the manager's device");
+  TORCH_CHECK(layer_idx >= 0 && layer_idx < mgr->num_layers(), "mega_attend_kv: layer_idx out of range");
+  TORCH_CHECK(current_t_list.dtype() == at::kLong && current_t_list.dim() == 1 && current_t_list.numel() > 0,
+              "mega_attend_kv: current_t_list must be a non-empty 1D int64 tensor");
+  auto tl = current_t_list.to(at::kCPU).contiguous();
+  const int64_t C = tl.numel();
+  TORCH_CHECK(C <= mgr->max_attend_chunks(), "mega_attend_kv: ", C, " chunks exceed max_attend_chunks (",
+              mgr->max_attend_chunks(), ")");
+  pkv_rope_tables rt;
+  pkv_rope_tables *rope = rope_tables_or_null(freqs_ft_flat, freqs_fy_flat, freqs_fx_flat, rt, "mega_attend_kv");
+  pkv_remap rm{static_cast<int32_t>(sink_mode_code), static_cast<int32_t>(sink_clamp_min),
+               static_cast<int32_t>(sink_clamp_max), static_cast<int32_t>(decoupled_sink_lag), 0, 0, 1.0};
+  const pkv_geometry g = mgr->geometry();
+  const pkv_pools p = mgr->pools();
+  const pkv_plan_out ws = mgr->plan_workspace();
+  pkv_check(pkv_plan_pack(&g, &p, states_layer.data_ptr<uint8_t>(), static_cast<int32_t>(layer_idx),
+                          tl.data_ptr<int64_t>(), static_cast<int32_t>(C), &rm, rope, &ws,
+                          stream_for(states_layer)),
+            "mega_attend_kv");
+  return mgr->cu_seqlens_k().narrow(0, 0, C * mgr->num_heads() + 1);
+}
+
 }  // namespace adahead
 
 // ---------------------------------------------------------------------------
@@ -762,6 +817,9 @@ TORCH_LIBRARY(adahead, m) {
         "Tensor sink_caps_layer, Tensor(b!) committed_vc_layer, Tensor new_k, Tensor new_v, int layer, int t0, "
         "int pass_kind, int shift_pending, int spatial_width, bool has_merge_head) -> ()");
   m.def("update_descriptors(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, int frames) -> Tensor[]");
+  m.def("mega_attend_kv(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, Tensor states_layer, "
+        "int layer_idx, Tensor current_t_list, int sink_mode_code, int sink_clamp_min, int sink_clamp_max, "
+        "int decoupled_sink_lag, Tensor freqs_ft_flat, Tensor freqs_fy_flat, Tensor freqs_fx_flat) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(adahead, CUDA, m) {
@@ -782,6 +840,7 @@ TORCH_LIBRARY_IMPL(adahead, CompositeExplicitAutograd, m) {
   m.impl("mega_plan", adahead::mega_plan);
   m.impl("mega_plan_multi", adahead::mega_plan_multi);
   m.impl("update_descriptors", adahead::update_descriptors);
+  m.impl("mega_attend_kv", adahead::mega_attend_kv);
 }
 
 TORCH_LIBRARY_IMPL(adahead, Meta, m) {

@@ -57,6 +57,7 @@ class MegaCacheCtx:
     freq_parts_flat: tuple = None
     # per layer: t0 of the block whose recent shift is in the pool but not committed
     pending_block: list = field(default_factory=list)
+    cu_q: dict = field(default_factory=dict)
 
 
 class MegaCache:
@@ -147,6 +148,25 @@ class MegaCache:
             _ops.pyramidkv_pack(mgr, sk, sga, sl, dst)
         return cu
 
+    def attend_kv(self, current_start: int, num_chunks: int, freqs=None) -> torch.Tensor:
+        """Plan + layer offset + pack (+RoPE) in one op; returns cu_seqlens_k
+        [C*H+1] (a view of the manager's buffer, valid until the next call)."""
+        ctx = self.ctx
+        FSEQ = ctx.frame_seqlen
+        t_list = torch.arange(current_start // FSEQ, current_start // FSEQ + num_chunks, dtype=torch.int64)
+        eff = ctx.freqs if ctx.freqs is not None else freqs
+        if eff is not None:
+            parts = ctx.freq_parts_flat
+            if parts is None:
+                from .rope import flat_freq_parts
+                parts = ctx.freq_parts_flat = flat_freq_parts(eff, ctx.states_bytes.device)
+        else:
+            parts = (_ops._empty(torch.float32, ctx.states_bytes.device),) * 3
+        return _ops.ops().mega_attend_kv(ctx.mgr, self.states_bytes_for_layer, self.layer_idx, t_list,
+                                         _mega_state_ops._SINK_MODE.get(ctx.sink_time_mapping_mode, 0),
+                                         int(ctx.sink_time_clamp_min), int(ctx.sink_time_clamp_max),
+                                         int(ctx.decoupled_sink_time_lag), *parts)
+
     def attend(self, q: torch.Tensor, current_start: int, *, freqs=None, softmax_scale=None, causal=False,
                max_seqlen_k=None) -> torch.Tensor:
         """Attention of q [1, L_q, H, D] (RoPE applied) over the cache."""
@@ -156,8 +176,13 @@ class MegaCache:
         assert B == 1, "MegaCache.attend: B>1 not yet supported"
         assert L_q % FSEQ == 0, f"L_q ({L_q}) must be a multiple of FSEQ ({FSEQ})"
         C = L_q // FSEQ
-        cu_k = self.pack(self.plan(current_start, C), freqs)
-        cu_q = torch.arange(0, L_q + 1, FSEQ, dtype=torch.int32, device=q.device)
+        if C <= int(ctx.mgr.max_attend_chunks()):
+            cu_k = self.attend_kv(current_start, C, freqs)
+        else:  # more chunks than the fused plan buffers hold: the reference op sequence (raises on overflow)
+            cu_k = self.pack(self.plan(current_start, C), freqs)
+        cu_q = ctx.cu_q.get(L_q)
+        if cu_q is None or cu_q.device != q.device:
+            cu_q = ctx.cu_q[L_q] = torch.arange(0, L_q + 1, FSEQ, dtype=torch.int32, device=q.device)
         qb = q[0] if q.dtype == torch.bfloat16 else q[0].to(torch.bfloat16)
         out = _ops.ragged_attention(qb, ctx.mgr.k_flat_out().view(-1, D), ctx.mgr.v_flat_out().view(-1, D), cu_q,
                                     cu_k, FSEQ, softmax_scale, kv_per_head=True, causal=causal)

@@ -77,6 +77,13 @@ def _compare_attend(cache, ref: O.MegaCacheRef, layer, start, chunks, q_u16, whe
     assert np.array_equal(to_np(mgr.k_flat_out()).reshape(-1, D)[:total], want["k"]), f"{where}: packed K differs"
     assert np.array_equal(to_np(mgr.v_flat_out()).reshape(-1, D)[:total], want["v"]), f"{where}: packed V differs"
     assert np.array_equal(to_np(mgr.pos_flat_out())[:total], want["pos"]), f"{where}: packed pos differs"
+    # the fused op MegaCache.attend uses (plan + layer offset + pack in one call) gives the same bytes
+    mgr.k_flat_out().zero_()
+    cu_fused = cache.attend_kv(start, chunks)
+    assert np.array_equal(to_np(cu_fused), want["cu"][:n_pairs + 1]), f"{where}: fused cu_seqlens_k differs"
+    assert np.array_equal(to_np(mgr.k_flat_out()).reshape(-1, D)[:total], want["k"]), f"{where}: fused K differs"
+    assert np.array_equal(to_np(mgr.v_flat_out()).reshape(-1, D)[:total], want["v"]), f"{where}: fused V differs"
+    assert np.array_equal(to_np(mgr.pos_flat_out())[:total], want["pos"]), f"{where}: fused pos differs"
     q = to_dev(q_u16).view(torch.bfloat16).view(1, chunks * FS, H, D)
     out = cache.attend(q, start)
     cu_q = np.arange(0, chunks * FS + 1, FS)
