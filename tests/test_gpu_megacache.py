@@ -185,3 +185,73 @@ def test_flash_attn_varlen_swap_point_matches_float64():
                                                           vf[cu_k[b]:cu_k[b + 1], h])
     err = np.abs(out.float().cpu().numpy() - exp)
     assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
+
+
+# ---------------------------------------------------------------------------
+# the reference's own MegaCache scenarios (tests/test_mega_cache_noisy_clean.py:41-231)
+# ---------------------------------------------------------------------------
+def _single_head_caches(comp, max_sink=3, max_middle=8, max_recent=4, D=16, FSEQ=4):
+    from pyramidkv._mega_cache import build_mega_caches
+    return build_mega_caches(1, 1, D, FSEQ, max_sink, max_middle, max_recent, [[comp]], device=DEV,
+                             kv_dtype="bfloat16")
+
+
+def _states(cache, H):
+    from pyramidkv import _mega_state_ops as S
+    return S.unpack_states(cache.states_bytes_for_layer.cpu().numpy().view(S.PER_HEAD_STATE_DTYPE).reshape(H).copy())
+
+
+def test_reference_noisy_iterations_then_clean_commits():
+    from pyramidkv.base import HeadComposition, StrideStrategy
+    H, D, FSEQ, F = 1, 16, 4, 3
+    cache = _single_head_caches(HeadComposition("stride", 1, 3, 4, [StrideStrategy(interval=1, capacity=8)]))[0]
+    torch.manual_seed(7)
+    mk = lambda: torch.randn(1, F * FSEQ, H, D, dtype=torch.bfloat16, device=DEV)
+    vc = cache.ctx.mgr.valid_count()
+    for i in range(4):
+        cache.update(mk(), mk(), current_start=0, cache_update_mode="noisy")
+        assert int(vc[0, 0, 0].item()) == F
+        assert int(cache.ctx.committed_vc[0, 0, 0].item()) == 0
+    assert _states(cache, H)[0].tkey_count == 0
+    ck, cv = mk(), mk()
+    cache.update(ck, cv, current_start=0, cache_update_mode="clean")
+    assert int(vc[0, 0, 0].item()) == F and int(cache.ctx.committed_vc[0, 0, 0].item()) == F
+    assert torch.equal(cache.ctx.mgr.sink_k_pool()[0, 0, 0], ck.view(1, F, FSEQ, H, D)[0, 0, :, 0, :])
+    assert _states(cache, H)[0].tkey_count == F
+
+
+def test_reference_block_2_noisy_uses_block_1_committed_baseline():
+    from pyramidkv.base import HeadComposition, StrideStrategy
+    H, D, FSEQ, F = 1, 16, 4, 3
+    cache = _single_head_caches(HeadComposition("stride", 1, 3, 4, [StrideStrategy(interval=1, capacity=8)]))[0]
+    torch.manual_seed(11)
+    mk = lambda: torch.randn(1, F * FSEQ, H, D, dtype=torch.bfloat16, device=DEV)
+    cache.update(mk(), mk(), current_start=0, cache_update_mode="clean")
+    assert int(cache.ctx.committed_vc[0, 0, 0].item()) == 3 and int(cache.ctx.committed_vc[0, 0, 2].item()) == 0
+    cache.update(mk(), mk(), current_start=3 * FSEQ, cache_update_mode="noisy")
+    vc = cache.ctx.mgr.valid_count()
+    assert int(vc[0, 0, 2].item()) == 3 and int(cache.ctx.committed_vc[0, 0, 2].item()) == 0
+    kb = mk()
+    cache.update(kb, mk(), current_start=3 * FSEQ, cache_update_mode="noisy")
+    assert int(vc[0, 0, 2].item()) == 3 and int(cache.ctx.committed_vc[0, 0, 2].item()) == 0
+    assert torch.equal(cache.ctx.mgr.recent_k_pool()[0, 0, :3], kb.view(F, FSEQ, H, D)[:, :, 0, :])
+
+
+def test_reference_recent_fifo_no_noisy_contamination():
+    from pyramidkv.base import HeadComposition, RecentStrategy
+    H, D, FSEQ, F = 1, 16, 4, 3
+    cache = _single_head_caches(HeadComposition("recent_only", -1, 1, 4, [RecentStrategy()]), max_sink=1)[0]
+    torch.manual_seed(101)
+    mk = lambda: torch.randn(1, F * FSEQ, H, D, dtype=torch.bfloat16, device=DEV)
+    clean = [(mk(), mk()) for _ in range(3)]
+    for b in range(2):
+        cache.update(*clean[b], current_start=b * F * FSEQ, cache_update_mode="clean")
+    before = cache.ctx.mgr.recent_k_pool()[0].clone()
+    noisy = [(mk(), mk()) for _ in range(3)]
+    for k_n, v_n in noisy:
+        cache.update(k_n, v_n, current_start=2 * F * FSEQ, cache_update_mode="noisy")
+    cache.update(*clean[2], current_start=2 * F * FSEQ, cache_update_mode="clean")
+    after = cache.ctx.mgr.recent_k_pool()[0]
+    assert torch.equal(after[0, 0], before[0, 3])
+    for k_n, _ in noisy:
+        assert not torch.equal(after[0, 0], k_n.view(1, F, FSEQ, H, D)[0, F - 1, :, 0, :])
