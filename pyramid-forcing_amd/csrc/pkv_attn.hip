@@ -278,6 +278,249 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Two waves per SIMD.  A workgroup of 8 waves owns 256 query rows (32 per
+// wave) of one (query sequence, head) pair, so every SIMD runs two waves
+// whose MFMA and softmax phases overlap; each wave stays within 256
+// registers.  K and V^T tiles of 64 keys are double-buffered in LDS with one
+// barrier per tile: waves 0-3 stage K rows (16-byte loads), waves 4-7 stage V
+// and transpose it in registers.  Global loads for tile t+2 are issued while
+// tile t is consumed.  Inside a tile the QK^T product of the second 32-key
+// block is issued before the softmax of the first.
+//
+// The softmax keeps its running maximum in log2 units and moves it only when
+// a new block exceeds it by more than kLazy (probabilities stay <= 2^kLazy,
+// far inside fp32 and bf16 range); O and the row sums are rescaled only
+// then.  The final O / l is the exact softmax either way.
+// ---------------------------------------------------------------------------
+constexpr int kWaves2 = 8;
+constexpr int kThreads2 = 64 * kWaves2;
+constexpr float kLazy = 8.0f;
+
+template <int D>
+__global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
+  constexpr int BQ = 32 * kWaves2;
+  constexpr int DS = D / 16;
+  constexpr int DB = D / 32;
+  constexpr int KS = D + 8;
+  constexpr int VS = kBK + 8;
+  constexpr int KCH = D / 8;
+  constexpr int KLD = kBK * KCH / 256;  // 16-byte K loads per thread of waves 0-3
+  static_assert(KLD * 256 == kBK * KCH, "K tile split");
+  constexpr int VGRP = kBK / 4;
+  constexpr int VPAIRS = VGRP * KCH;    // (4-key group, 16-byte chunk) pairs, one per thread of waves 4-7
+  static_assert(VPAIRS <= 256, "V tile split");
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VS];
+
+  const int wg = xcd_remap(blockIdx.x, p.n_wg);
+  const int seq = wg / p.q_tiles, qt = wg % p.q_tiles;
+  const int b = seq / p.Hq, h = seq % p.Hq;
+  const int q_begin = p.cu_q[b];
+  const int Lq = p.cu_q[b + 1] - q_begin;
+  const int q0 = qt * BQ;
+  if (q0 >= Lq) return;
+  const int kv_idx = p.kv_per_head ? seq : b;
+  const int k_begin = p.cu_k[kv_idx];
+  const int Lk = p.cu_k[kv_idx + 1] - k_begin;
+
+  const uint16_t *qp = p.q + static_cast<int64_t>(q_begin) * p.q_tok + h * p.q_head;
+  const int64_t kv_off = static_cast<int64_t>(k_begin) * p.kv_tok + (p.kv_per_head ? 0 : h * p.kv_head);
+  const uint16_t *kp = p.k + kv_off;
+  const uint16_t *vp = p.v + kv_off;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int row_q = q0 + wave * 32 + lq;
+  const float c = p.scale_log2;
+
+  bf16x8 qr[DS];
+#pragma unroll
+  for (int s = 0; s < DS; ++s) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row_q < Lq) v = ldg16(qp + static_cast<int64_t>(row_q) * p.q_tok + 16 * s + 8 * hf);
+    qr[s] = as_bf16x8(v);
+  }
+  f32x16 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  // staging roles
+  const bool k_loader = tid < 256;
+  const int vt = tid - 256;
+  const bool v_loader = !k_loader && vt < VPAIRS;
+  const int vgrp = v_loader ? vt % VGRP : 0, vch = v_loader ? vt / VGRP : 0;
+  uint4 st[4];
+  static_assert(KLD <= 4, "staging registers");
+
+  auto load_tile = [&](int kt) {
+    const int kbase = kt * kBK;
+    if (k_loader) {
+#pragma unroll
+      for (int r = 0; r < KLD; ++r) {
+        const int idx = tid + r * 256;
+        const int row = idx / KCH, ch = idx % KCH;
+        const int key = kbase + row;
+        st[r] = key < Lk ? ldg16(kp + static_cast<int64_t>(key) * p.kv_tok + ch * 8) : make_uint4(0, 0, 0, 0);
+      }
+    } else if (v_loader) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = kbase + vgrp * 4 + j;
+        st[j] = key < Lk ? ldg16(vp + static_cast<int64_t>(key) * p.kv_tok + vch * 8) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    if (k_loader) {
+#pragma unroll
+      for (int r = 0; r < KLD; ++r) {
+        const int idx = tid + r * 256;
+        const int row = idx / KCH, ch = idx % KCH;
+        *reinterpret_cast<uint4 *>(&Ks[buf][row * KS + ch * 8]) = st[r];
+      }
+    } else if (v_loader) {
+      const uint32_t w0[4] = {st[0].x, st[0].y, st[0].z, st[0].w};
+      const uint32_t w1[4] = {st[1].x, st[1].y, st[1].z, st[1].w};
+      const uint32_t w2[4] = {st[2].x, st[2].y, st[2].z, st[2].w};
+      const uint32_t w3[4] = {st[3].x, st[3].y, st[3].z, st[3].w};
+      const int col = vt_pos(vgrp * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo01 = (w0[e] & 0xffffu) | (w1[e] << 16);
+        const uint32_t lo23 = (w2[e] & 0xffffu) | (w3[e] << 16);
+        const uint32_t hi01 = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
+        const uint32_t hi23 = (w2[e] >> 16) | (w3[e] & 0xffff0000u);
+        *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e) * VS + col]) = make_uint2(lo01, lo23);
+        *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e + 1) * VS + col]) = make_uint2(hi01, hi23);
+      }
+    }
+  };
+
+  auto qk = [&](int buf, int kb) {
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(&Ks[buf][(kb * 32 + lq) * KS + 16 * s + 8 * hf]));
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qr[s], acc, 0, 0, 0);
+    }
+    return acc;
+  };
+
+  // softmax of one 32-key block and O^T += V^T P^T
+  auto consume = [&](f32x16 sacc, int buf, int kb, int kb0) {
+    if (kb0 + 32 > Lk) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb0 + 8 * (i / 4) + 4 * hf + (i % 4);
+        if (key >= Lk) sacc[i] = -INFINITY;
+      }
+    }
+    float mx = sacc[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
+    mx = fmaxf(mx, xor32(mx)) * c;
+    const bool move = mx > m + kLazy || m == -INFINITY;
+    float alpha = 1.0f;
+    if (move) {
+      alpha = __builtin_amdgcn_exp2f(m - mx);
+      m = mx;
+    }
+    float ps = 0.0f;
+    bf16x8 pb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[8 * ks + j], c, -m));
+        ps += e;
+        pb[ks][j] = static_cast<__bf16>(e);
+      }
+    l = l * alpha + ps;
+    if (__any(move)) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const bf16x8 a =
+            as_bf16x8(*reinterpret_cast<const uint4 *>(&Vt[buf][(db * 32 + lq) * VS + kb * 32 + 16 * ks + 8 * hf]));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
+      }
+  };
+
+  const int n_tiles = (Lk + kBK - 1) / kBK;
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+    if (n_tiles > 1) load_tile(1);
+  }
+  for (int kt = 0; kt < n_tiles; ++kt) {
+    const int buf = kt & 1;
+    __syncthreads();
+    if (kt + 1 < n_tiles) store_tile(buf ^ 1);
+    if (kt + 2 < n_tiles) load_tile(kt + 2);
+    const int kb0 = kt * kBK;
+    const f32x16 s0 = qk(buf, 0);
+    if (kb0 + 32 < Lk) {
+      const f32x16 s1 = qk(buf, 1);
+      consume(s0, buf, 0, kb0);
+      consume(s1, buf, 1, kb0 + 32);
+    } else {
+      consume(s0, buf, 0, kb0);
+    }
+  }
+
+  uint16_t *op = p.o + static_cast<int64_t>(q_begin) * p.o_tok + h * p.o_head;
+  const float lt = l + xor32(l);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (row_q < Lq) {
+    uint16_t *orow = op + static_cast<int64_t>(row_q) * p.o_tok;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<__bf16>(o[db][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4 *>(orow + d) = v;
+      }
+  }
+}
+
+template <int D>
+static int launch_attn2(const pkv_attn_args *a, hipStream_t st) {
+  constexpr int BQ = 32 * kWaves2;
+  AttnParams p;
+  p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o;
+  p.cu_q = a->cu_seqlens_q; p.cu_k = a->cu_seqlens_k;
+  p.Hq = a->num_heads_q;
+  p.kv_per_head = a->kv_per_head;
+  p.q_tiles = (a->max_seqlen_q + BQ - 1) / BQ;
+  const int64_t n = static_cast<int64_t>(p.q_tiles) * a->num_batches * a->num_heads_q;
+  if (n > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: grid too large");
+  p.n_wg = static_cast<int>(n);
+  p.q_tok = a->q_tok_stride; p.q_head = a->q_head_stride;
+  p.kv_tok = a->kv_tok_stride; p.kv_head = a->kv_head_stride;
+  p.o_tok = a->o_tok_stride; p.o_head = a->o_head_stride;
+  p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
+  if (p.n_wg == 0) return PKV_OK;
+  hipLaunchKernelGGL((attn_fwd2_kernel<D>), dim3(p.n_wg), dim3(kThreads2), 0, st, p);
+  return check_launch("attn_fwd2_kernel");
+}
+
 template <int D, int QB>
 static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   constexpr int BQ = 32 * QB * kAttnWaves;
@@ -316,8 +559,8 @@ extern "C" int pkv_ragged_attn_fwd(const pkv_attn_args *a, pkv_stream_t stream) 
     return fail(PKV_ERR_INVALID, "ragged_attn: strides must keep 16-byte rows aligned");
   hipStream_t st = as_stream(stream);
   switch (a->head_dim) {
-    case 128: return launch_attn<128, 2>(a, st);
-    case 64: return launch_attn<64, 2>(a, st);
+    case 128: return launch_attn2<128>(a, st);
+    case 64: return launch_attn2<64>(a, st);
     default: return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: head_dim %d (supported: 64, 128)", a->head_dim);
   }
 }
