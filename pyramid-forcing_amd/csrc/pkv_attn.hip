@@ -53,9 +53,29 @@ __device__ inline bool tid_in_range(int n) { return static_cast<int>(threadIdx.x
 
 __device__ inline uint4 ldg16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
+// Buffer resource word 3 for gfx9-family raw buffers (32-bit data format,
+// no swizzle); out-of-range loads return zero.
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ inline bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ inline float xor32(float x) { return __shfl_xor(x, 32); }
+
+// max / sum of x over lanes l and l^32 (v_permlane32_swap exchanges the two
+// half-waves of its operands)
+__device__ inline float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // position of key k (0..63) of a tile inside its V^T row: swap bits 2 and 3
 __device__ inline int vt_pos(int k) { return (k & ~0xC) | ((k & 4) << 1) | ((k & 8) >> 1); }
@@ -349,8 +369,19 @@ __global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
     for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
   float m = -INFINITY, l = 0.0f;
 
-  // staging roles
-  const bool k_loader = tid < 256;
+  // K/V reads go through buffer resources bounded at the sequence's last
+  // row: rows past Lk read as zero without a branch, and no access can leave
+  // the sequence.
+  const int64_t kv_bytes = static_cast<int64_t>(Lk) * p.kv_tok * 2;
+  const int nrec = static_cast<int>(kv_bytes < 0x7fffffff ? kv_bytes : 0x7fffffff);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kp), 0, nrec, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vp), 0, nrec, kRsrcWord3);
+  const int row_bytes = static_cast<int>(p.kv_tok) * 2;
+
+  // staging roles, decided per wave (readfirstlane makes the uniformity
+  // visible to the compiler, so each role keeps its own scalar resource)
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const bool k_loader = wave_u < 4;
   const int vt = tid - 256;
   const bool v_loader = !k_loader && vt < VPAIRS;
   const int vgrp = v_loader ? vt % VGRP : 0, vch = v_loader ? vt / VGRP : 0;
@@ -364,15 +395,11 @@ __global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
       for (int r = 0; r < KLD; ++r) {
         const int idx = tid + r * 256;
         const int row = idx / KCH, ch = idx % KCH;
-        const int key = kbase + row;
-        st[r] = key < Lk ? ldg16(kp + static_cast<int64_t>(key) * p.kv_tok + ch * 8) : make_uint4(0, 0, 0, 0);
+        st[r] = bload16(rk, (kbase + row) * row_bytes + ch * 16);
       }
     } else if (v_loader) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = kbase + vgrp * 4 + j;
-        st[j] = key < Lk ? ldg16(vp + static_cast<int64_t>(key) * p.kv_tok + vch * 8) : make_uint4(0, 0, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j) st[j] = bload16(rv, (kbase + vgrp * 4 + j) * row_bytes + vch * 16);
     }
   };
   auto store_tile = [&](int buf) {
@@ -413,19 +440,20 @@ __global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
     return acc;
   };
 
-  // softmax of one 32-key block and O^T += V^T P^T
-  auto consume = [&](f32x16 sacc, int buf, int kb, int kb0) {
-    if (kb0 + 32 > Lk) {
+  // softmax of one 64-key tile (two 32-key S^T blocks) and O^T += V^T P^T
+  auto consume = [&](f32x16 s0, f32x16 s1, int buf, int kb0) {
+    if (kb0 + kBK > Lk) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = kb0 + 8 * (i / 4) + 4 * hf + (i % 4);
-        if (key >= Lk) sacc[i] = -INFINITY;
+        if (key >= Lk) s0[i] = -INFINITY;
+        if (key + 32 >= Lk) s1[i] = -INFINITY;
       }
     }
-    float mx = sacc[0];
+    float mx = fmaxf(s0[0], s1[0]);
 #pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[i]);
-    mx = fmaxf(mx, xor32(mx)) * c;
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, fmaxf(s0[i], s1[i]));
+    mx = half_max(mx) * c;
     const bool move = mx > m + kLazy || m == -INFINITY;
     float alpha = 1.0f;
     if (move) {
@@ -433,28 +461,30 @@ __global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
       m = mx;
     }
     float ps = 0.0f;
-    bf16x8 pb[2];
+    bf16x8 pb[4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[8 * ks + j], c, -m));
+        const float sv = ks < 2 ? s0[8 * ks + j] : s1[8 * (ks - 2) + j];
+        const float e = __builtin_amdgcn_exp2f(fmaf(sv, c, -m));
         ps += e;
         pb[ks][j] = static_cast<__bf16>(e);
       }
     l = l * alpha + ps;
     if (__any(move)) {
+      // in place (tied operands), so the accumulators keep their registers
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        for (int i = 0; i < 16; ++i) asm volatile("v_mul_f32_e32 %0, %1, %0" : "+v"(o[db][i]) : "v"(alpha));
     }
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const bf16x8 a =
-            as_bf16x8(*reinterpret_cast<const uint4 *>(&Vt[buf][(db * 32 + lq) * VS + kb * 32 + 16 * ks + 8 * hf]));
+            as_bf16x8(*reinterpret_cast<const uint4 *>(&Vt[buf][(db * 32 + lq) * VS + 16 * ks + 8 * hf]));
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
       }
   };
@@ -470,19 +500,13 @@ __global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
     __syncthreads();
     if (kt + 1 < n_tiles) store_tile(buf ^ 1);
     if (kt + 2 < n_tiles) load_tile(kt + 2);
-    const int kb0 = kt * kBK;
     const f32x16 s0 = qk(buf, 0);
-    if (kb0 + 32 < Lk) {
-      const f32x16 s1 = qk(buf, 1);
-      consume(s0, buf, 0, kb0);
-      consume(s1, buf, 1, kb0 + 32);
-    } else {
-      consume(s0, buf, 0, kb0);
-    }
+    const f32x16 s1 = qk(buf, 1);
+    consume(s0, s1, buf, kt * kBK);
   }
 
   uint16_t *op = p.o + static_cast<int64_t>(q_begin) * p.o_tok + h * p.o_head;
-  const float lt = l + xor32(l);
+  const float lt = half_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   if (row_q < Lq) {
     uint16_t *orow = op + static_cast<int64_t>(row_q) * p.o_tok;
