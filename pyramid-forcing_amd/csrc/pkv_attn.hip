@@ -313,23 +313,24 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnParams p) {
 // far inside fp32 and bf16 range); O and the row sums are rescaled only
 // then.  The final O / l is the exact softmax either way.
 // ---------------------------------------------------------------------------
-constexpr int kWaves2 = 8;
-constexpr int kThreads2 = 64 * kWaves2;
+constexpr int kWaves2 = 4;
 constexpr float kLazy = 8.0f;
 
-template <int D>
-__global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
-  constexpr int BQ = 32 * kWaves2;
+template <int D, int W>
+__global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
+  constexpr int BQ = 32 * W;
+  constexpr int HT = 32 * W;  // threads per staging role (half the workgroup)
   constexpr int DS = D / 16;
   constexpr int DB = D / 32;
   constexpr int KS = D + 8;
   constexpr int VS = kBK + 8;
   constexpr int KCH = D / 8;
-  constexpr int KLD = kBK * KCH / 256;  // 16-byte K loads per thread of waves 0-3
-  static_assert(KLD * 256 == kBK * KCH, "K tile split");
+  constexpr int KLD = kBK * KCH / HT;  // 16-byte K loads per thread of the K half
+  static_assert(KLD * HT == kBK * KCH, "K tile split");
   constexpr int VGRP = kBK / 4;
-  constexpr int VPAIRS = VGRP * KCH;    // (4-key group, 16-byte chunk) pairs, one per thread of waves 4-7
-  static_assert(VPAIRS <= 256, "V tile split");
+  constexpr int VPAIRS = VGRP * KCH;    // (4-key group, 16-byte chunk) pairs of the V half
+  constexpr int VPP = (VPAIRS + HT - 1) / HT;  // pairs per thread
+  static_assert(VPP * 4 <= 8 && KLD <= 8, "staging registers");
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * KS];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VS];
 
@@ -381,49 +382,61 @@ __global__ void __launch_bounds__(kThreads2) attn_fwd2_kernel(AttnParams p) {
   // staging roles, decided per wave (readfirstlane makes the uniformity
   // visible to the compiler, so each role keeps its own scalar resource)
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const bool k_loader = wave_u < 4;
-  const int vt = tid - 256;
-  const bool v_loader = !k_loader && vt < VPAIRS;
-  const int vgrp = v_loader ? vt % VGRP : 0, vch = v_loader ? vt / VGRP : 0;
-  uint4 st[4];
-  static_assert(KLD <= 4, "staging registers");
+  const bool k_loader = wave_u < W / 2;
+  const int vt = tid - HT;
+  uint4 st[8];
 
   auto load_tile = [&](int kt) {
     const int kbase = kt * kBK;
     if (k_loader) {
 #pragma unroll
       for (int r = 0; r < KLD; ++r) {
-        const int idx = tid + r * 256;
+        const int idx = tid + r * HT;
         const int row = idx / KCH, ch = idx % KCH;
         st[r] = bload16(rk, (kbase + row) * row_bytes + ch * 16);
       }
-    } else if (v_loader) {
+    } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) st[j] = bload16(rv, (kbase + vgrp * 4 + j) * row_bytes + vch * 16);
+      for (int pp = 0; pp < VPP; ++pp) {
+        const int pair = vt + pp * HT;
+        if (VPAIRS % HT == 0 || pair < VPAIRS) {
+          const int vgrp = pair % VGRP, vch = pair / VGRP;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) st[pp * 4 + j] = bload16(rv, (kbase + vgrp * 4 + j) * row_bytes + vch * 16);
+        }
+      }
     }
   };
   auto store_tile = [&](int buf) {
     if (k_loader) {
 #pragma unroll
       for (int r = 0; r < KLD; ++r) {
-        const int idx = tid + r * 256;
+        const int idx = tid + r * HT;
         const int row = idx / KCH, ch = idx % KCH;
         *reinterpret_cast<uint4 *>(&Ks[buf][row * KS + ch * 8]) = st[r];
       }
-    } else if (v_loader) {
-      const uint32_t w0[4] = {st[0].x, st[0].y, st[0].z, st[0].w};
-      const uint32_t w1[4] = {st[1].x, st[1].y, st[1].z, st[1].w};
-      const uint32_t w2[4] = {st[2].x, st[2].y, st[2].z, st[2].w};
-      const uint32_t w3[4] = {st[3].x, st[3].y, st[3].z, st[3].w};
-      const int col = vt_pos(vgrp * 4);
+    } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t lo01 = (w0[e] & 0xffffu) | (w1[e] << 16);
-        const uint32_t lo23 = (w2[e] & 0xffffu) | (w3[e] << 16);
-        const uint32_t hi01 = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
-        const uint32_t hi23 = (w2[e] >> 16) | (w3[e] & 0xffff0000u);
-        *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e) * VS + col]) = make_uint2(lo01, lo23);
-        *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e + 1) * VS + col]) = make_uint2(hi01, hi23);
+      for (int pp = 0; pp < VPP; ++pp) {
+        const int pair = vt + pp * HT;
+        if (VPAIRS % HT == 0 || pair < VPAIRS) {
+          const int vgrp = pair % VGRP, vch = pair / VGRP;
+          const uint4 *q4 = st + pp * 4;
+          const uint32_t w0[4] = {q4[0].x, q4[0].y, q4[0].z, q4[0].w};
+          const uint32_t w1[4] = {q4[1].x, q4[1].y, q4[1].z, q4[1].w};
+          const uint32_t w2[4] = {q4[2].x, q4[2].y, q4[2].z, q4[2].w};
+          const uint32_t w3[4] = {q4[3].x, q4[3].y, q4[3].z, q4[3].w};
+          const int col = vt_pos(vgrp * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t lo01 = (w0[e] & 0xffffu) | (w1[e] << 16);
+            const uint32_t lo23 = (w2[e] & 0xffffu) | (w3[e] << 16);
+            const uint32_t hi01 = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
+            const uint32_t hi23 = (w2[e] >> 16) | (w3[e] & 0xffff0000u);
+            *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e) * VS + col]) = make_uint2(lo01, lo23);
+            *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e + 1) * VS + col]) = make_uint2(hi01, hi23);
+          }
+        }
       }
     }
   };
@@ -541,7 +554,7 @@ static int launch_attn2(const pkv_attn_args *a, hipStream_t st) {
   p.o_tok = a->o_tok_stride; p.o_head = a->o_head_stride;
   p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   if (p.n_wg == 0) return PKV_OK;
-  hipLaunchKernelGGL((attn_fwd2_kernel<D>), dim3(p.n_wg), dim3(kThreads2), 0, st, p);
+  hipLaunchKernelGGL((attn_fwd2_kernel<D, kWaves2>), dim3(p.n_wg), dim3(64 * kWaves2), 0, st, p);
   return check_launch("attn_fwd2_kernel");
 }
 
