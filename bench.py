@@ -32,6 +32,7 @@ METRIC = "ragged-attn TFLOP/s + cache update/pack GB/s (% roofline); latent chun
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 FSEQ, H, L, D, QTOK = 1560, 12, 30, 128, 4680
+ATTN_KERNEL = "attn_fwd_kernel<128>"
 
 
 def config2_lengths(seed: int = 0):
@@ -434,6 +435,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true", help="skip the config-3 / config-4 measurements")
+    ap.add_argument("--workload", choices=["all", "attn", "cache", "merge", "copy"], default="all",
+                    help="run one workload alone and print its timing (for profiler runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the pyramid-cache path needs no exchange between GPUs and this build "
@@ -441,6 +444,9 @@ def main():
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if args.workload != "all":
+        print(json.dumps(single_workload(args)))
+        return
 
     r = bench_attention(args.steps, args.warmup)
     tflops = r["flops"] / (r["kernel_ms"] * 1e-3) / 1e12
@@ -462,7 +468,7 @@ def main():
                    "kv_tokens_total": int(r["lk"].sum()), "labels_seed": 0, "flop_per_step": r["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "attn_fwd_kernel<128,2>", "avg_launch_ms": round(r["kernel_ms"], 4)},
+                     "kernel": ATTN_KERNEL, "avg_launch_ms": round(r["kernel_ms"], 4)},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_attention(r["lk"])
@@ -471,6 +477,30 @@ def main():
     if not args.headline_only:
         line["secondary"] = secondary(args)
     print(json.dumps(line))
+
+
+def single_workload(args):
+    """One workload alone (no CPU legs), for rocprofv3 runs: attn = config-2
+    launches, cache = config-3 steps, merge = config-4 steps, copy = a
+    device-to-device copy of 1 GiB (the reference kernel that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters: 1 GiB read + 1 GiB written)."""
+    import torch
+    if args.workload == "attn":
+        r = bench_attention(args.steps, args.warmup)
+        return {"workload": "attn", "kernel": ATTN_KERNEL, "avg_launch_ms": r["kernel_ms"], "flop": r["flops"]}
+    if args.workload == "cache":
+        c3 = bench_cache_step(args.steps, args.warmup)
+        return {"workload": "cache", "eager_ms": c3["eager_ms"], "graph_ms": c3["graph_ms"],
+                "bytes_per_step": c3["total_bytes"], "pack_bytes_layer0": c3["packed"][0] * (2 * ROW + 2 * ROW + 48)}
+    if args.workload == "merge":
+        c4 = bench_merge(args.steps, args.warmup)
+        return {"workload": "merge", "ms": c4["ms"], "bytes_per_step": c4["bytes"]}
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(max(1, args.steps)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"workload": "copy", "bytes_read_per_launch": src.numel() * 2, "bytes_written_per_launch": dst.numel() * 2}
 
 
 def secondary(args):

@@ -1,24 +1,35 @@
 // Ragged-cache attention for gfx950: bf16 inputs, fp32 online softmax and
-// accumulation, MFMA v_mfma_f32_32x32x16_bf16.
+// accumulation, MFMA v_mfma_f32_32x32x16_bf16.  Replaces the reference's
+// flash_attn_varlen_func call (pyramidkv/_mega_cache.py:540-559).
 //
-// Work decomposition.  A workgroup (4 waves) owns 32*QB*4 query rows of one
-// (query sequence, head) pair and streams that pair's keys through LDS in
-// tiles of 64.  Each wave owns 32*QB query rows.
+// Work decomposition.  A workgroup of 4 waves owns 128 query rows (32 per
+// wave) of one (query sequence, head) pair and streams that pair's keys in
+// tiles of 64 through double-buffered LDS, one barrier per tile.  Two
+// workgroups share a CU (each wave stays within 256 registers), so every SIMD
+// runs two waves whose MFMA and softmax phases interleave.  All 256 threads
+// stage both K and V: 16-byte buffer loads bounded at the sequence's last row
+// (rows past the end read as zero), prefetched one tile ahead, stored
+// row-major into LDS with 16-byte stores.
 //
-// Operand arrangement.  The wave computes S^T = K * Q^T (A = K rows read from
-// LDS, B = Q^T kept in registers for the whole loop), so the 32x32 MFMA
-// result gives every lane one query column and 16 keys of it.  The
-// probabilities are then consumed as the B operand of O^T = V^T * P^T
-// straight from registers: for a k-step of 16 keys, lane half hf holds keys
-// {16ks + 8*(j/4) + 4*hf + j%4 : j < 8}, and V^T is stored in LDS with the
-// two middle bits of each 16-key group swapped so those 8 keys are one
-// contiguous 16-byte read.  O^T's accumulator again gives every lane one
-// query column, so the running max / sum and the rescale of O are lane-local
-// (one xor-32 exchange per row statistic).
+// Operand arrangement.  The wave computes S^T = K * Q^T (A = K rows read
+// from LDS, B = Q^T kept in registers), so the 32x32 MFMA result gives every
+// lane one query column and 16 keys of it: lane half hf holds keys
+// {8*(i/4) + 4*hf + i%4 : i < 16} of a 32-key block.  O^T = V^T * P^T then
+// takes P^T straight from those registers as the B operand (for each 16-key
+// step, the lane's 8 keys in that order) and V^T as the A operand, read from
+// the row-major V tile with the LDS transpose read ds_read_b64_tr_b16: in
+// every 16-lane group, lane j addresses V[k0 + j/4][d0 + 4*(j%4)] and lane i
+// receives V[k0 + r][d0 + i] for r = 0..3, i.e. one dim and four keys.
+// O^T's accumulator again gives every lane one query column, so the row
+// statistics need one half-wave exchange (v_permlane32_swap) and the rescale
+// of O is lane-local.
 //
-// Softmax runs in the log2 domain, s' = s * scale * log2(e), exp2 via
-// v_exp_f32; P is rounded to bf16 before the P*V product, row sums use the
-// unrounded fp32 values (the flash-attention scheme).
+// Softmax runs in the log2 domain (the scale is folded into one FMA before
+// v_exp_f32), keeps its running maximum per row and moves it only when a tile
+// exceeds it by more than kLazy: probabilities then stay <= 2^kLazy, far
+// inside fp32 and bf16 range, and the final O / l is the exact softmax.  P is
+// rounded to bf16 before the P*V product; row sums use the unrounded fp32
+// values (the flash-attention scheme).
 
 #include "pkv_common.h"
 
@@ -26,10 +37,13 @@ namespace pkv {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int kAttnWaves = 4;
-constexpr int kAttnThreads = 64 * kAttnWaves;
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kBK = 64;  // keys per LDS tile
+constexpr float kLazy = 8.0f;
 
 struct AttnParams {
   const uint16_t *q, *k, *v;
@@ -49,8 +63,6 @@ __device__ inline int xcd_remap(int i, int n) {
   return xcd < rem ? xcd * (base + 1) + k : rem * (base + 1) + (xcd - rem) * base + k;
 }
 
-__device__ inline bool tid_in_range(int n) { return static_cast<int>(threadIdx.x) < n; }
-
 __device__ inline uint4 ldg16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
 // Buffer resource word 3 for gfx9-family raw buffers (32-bit data format,
@@ -64,7 +76,11 @@ __device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, int byte_off) {
 
 __device__ inline bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-__device__ inline float xor32(float x) { return __shfl_xor(x, 32); }
+// transpose read of 4 x 16 bits (see the operand arrangement above)
+__device__ inline i16x4 lds_tr16(const uint16_t *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4 *)((__attribute__((address_space(3))) char *)(p)));
+}
 
 // max / sum of x over lanes l and l^32 (v_permlane32_swap exchanges the two
 // half-waves of its operands)
@@ -77,262 +93,17 @@ __device__ inline float half_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// position of key k (0..63) of a tile inside its V^T row: swap bits 2 and 3
-__device__ inline int vt_pos(int k) { return (k & ~0xC) | ((k & 4) << 1) | ((k & 8) >> 1); }
-
-template <int D, int QB>
-__global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(AttnParams p) {
-  constexpr int BQ = 32 * QB * kAttnWaves;
+template <int D>
+__global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
+  constexpr int BQ = 32 * kWaves;
   constexpr int DS = D / 16;  // k-steps of the QK^T product
   constexpr int DB = D / 32;  // 32-row blocks of O^T
-  constexpr int KS = D + 8;   // K row stride in LDS (elements); +16 B kills bank conflicts
-  constexpr int VS = kBK + 8; // V^T row stride in LDS (elements)
-  constexpr int KCH = D / 8;  // 16-byte chunks per K/V row
-  constexpr int KLD = kBK * KCH / kAttnThreads;  // 16-byte K loads per thread per tile
-  static_assert(KLD * kAttnThreads == kBK * KCH, "tile split");
-  constexpr int VGRP = kBK / 4;                   // 4-key groups per tile
-  static_assert(VGRP * KCH <= kAttnThreads, "V split");
-  const bool v_owner = tid_in_range(VGRP * KCH);
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VS];
-
-  const int wg = xcd_remap(blockIdx.x, p.n_wg);
-  const int seq = wg / p.q_tiles, qt = wg % p.q_tiles;
-  const int b = seq / p.Hq, h = seq % p.Hq;
-  const int q_begin = p.cu_q[b];
-  const int Lq = p.cu_q[b + 1] - q_begin;
-  const int q0 = qt * BQ;
-  if (q0 >= Lq) return;
-  const int kv_idx = p.kv_per_head ? seq : b;
-  const int k_begin = p.cu_k[kv_idx];
-  const int Lk = p.cu_k[kv_idx + 1] - k_begin;
-
-  const uint16_t *qp = p.q + static_cast<int64_t>(q_begin) * p.q_tok + h * p.q_head;
-  const int64_t kv_off = static_cast<int64_t>(k_begin) * p.kv_tok + (p.kv_per_head ? 0 : h * p.kv_head);
-  const uint16_t *kp = p.k + kv_off;
-  const uint16_t *vp = p.v + kv_off;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int lq = lane & 31, hf = lane >> 5;
-  const int wq0 = q0 + wave * 32 * QB;
-
-  // ---- Q^T operand, resident for the whole key loop
-  bf16x8 qr[QB][DS];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int row = wq0 + qb * 32 + lq;
-#pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (row < Lq) v = ldg16(qp + static_cast<int64_t>(row) * p.q_tok + 16 * s + 8 * hf);
-      qr[qb][s] = as_bf16x8(v);
-    }
-  }
-
-  f32x16 o[QB][DB];
-  float m[QB], l[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m[qb] = -INFINITY;
-    l[qb] = 0.0f;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[qb][db][i] = 0.0f;
-  }
-
-  // ---- global -> register staging of one K/V tile
-  uint4 kreg[KLD], vreg[4];
-  const int vgrp = tid % VGRP, vch = tid / VGRP;  // V: 4 keys x 8 dims per thread
-  auto load_tile = [&](int kt) {
-    const int kbase = kt * kBK;
-#pragma unroll
-    for (int r = 0; r < KLD; ++r) {
-      const int idx = tid + r * kAttnThreads;
-      const int row = idx / KCH, ch = idx % KCH;
-      const int key = kbase + row;
-      kreg[r] = key < Lk ? ldg16(kp + static_cast<int64_t>(key) * p.kv_tok + ch * 8) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int key = kbase + vgrp * 4 + j;
-      vreg[j] = (v_owner && key < Lk) ? ldg16(vp + static_cast<int64_t>(key) * p.kv_tok + vch * 8)
-                                      : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int r = 0; r < KLD; ++r) {
-      const int idx = tid + r * kAttnThreads;
-      const int row = idx / KCH, ch = idx % KCH;
-      *reinterpret_cast<uint4 *>(&Ks[row * KS + ch * 8]) = kreg[r];
-    }
-    if (!v_owner) return;
-    // transpose 4 keys x 8 dims into 8 rows of 4 keys
-    const uint32_t w0[4] = {vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w};
-    const uint32_t w1[4] = {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w};
-    const uint32_t w2[4] = {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w};
-    const uint32_t w3[4] = {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w};
-    const int col = vt_pos(vgrp * 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // dims 2e (low halves) and 2e+1 (high halves)
-      const uint32_t lo01 = (w0[e] & 0xffffu) | (w1[e] << 16);
-      const uint32_t lo23 = (w2[e] & 0xffffu) | (w3[e] << 16);
-      const uint32_t hi01 = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
-      const uint32_t hi23 = (w2[e] >> 16) | (w3[e] & 0xffff0000u);
-      *reinterpret_cast<uint2 *>(&Vt[(vch * 8 + 2 * e) * VS + col]) = make_uint2(lo01, lo23);
-      *reinterpret_cast<uint2 *>(&Vt[(vch * 8 + 2 * e + 1) * VS + col]) = make_uint2(hi01, hi23);
-    }
-  };
-
-  const int n_tiles = (Lk + kBK - 1) / kBK;
-  if (n_tiles > 0) load_tile(0);
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (kt + 1 < n_tiles) load_tile(kt + 1);
-
-    const int kbase = kt * kBK;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int kb0 = kbase + kb * 32;
-      if (kb0 >= Lk) break;
-      // ---- S^T = K Q^T for 32 keys
-      f32x16 sacc[QB];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sacc[qb][i] = 0.0f;
-#pragma unroll
-      for (int s = 0; s < DS; ++s) {
-        const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(&Ks[(kb * 32 + lq) * KS + 16 * s + 8 * hf]));
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qr[qb][s], sacc[qb], 0, 0, 0);
-      }
-
-      // ---- online softmax over the 32 keys
-      const bool full = kb0 + 32 <= Lk;
-      bf16x8 pb[2][QB];  // [ks][qb]
-      bool rescale = false;
-      float alpha[QB];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float sv = sacc[qb][i] * p.scale_log2;
-          if (!full) {
-            const int key = kb0 + 8 * (i / 4) + 4 * hf + (i % 4);
-            if (key >= Lk) sv = -INFINITY;
-          }
-          sacc[qb][i] = sv;
-          mx = fmaxf(mx, sv);
-        }
-        mx = fmaxf(mx, xor32(mx));
-        const float mnew = fmaxf(m[qb], mx);
-        const float mref = mnew == -INFINITY ? 0.0f : mnew;
-        alpha[qb] = __builtin_amdgcn_exp2f(m[qb] - mref);
-        rescale |= mnew > m[qb];
-        m[qb] = mnew;
-        float ps = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          bf16x8 v;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float e = __builtin_amdgcn_exp2f(sacc[qb][8 * ks + j] - mref);
-            ps += e;
-            v[j] = static_cast<__bf16>(e);
-          }
-          pb[ks][qb] = v;
-        }
-        l[qb] = l[qb] * alpha[qb] + ps;
-      }
-      if (__any(rescale)) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-          for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[qb][db][i] *= alpha[qb];
-      }
-
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const bf16x8 a =
-              as_bf16x8(*reinterpret_cast<const uint4 *>(&Vt[(db * 32 + lq) * VS + kb * 32 + 16 * ks + 8 * hf]));
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks][qb], o[qb][db], 0, 0, 0);
-        }
-    }
-  }
-
-  // ---- epilogue: O = O^T / l, rows of 4 consecutive dims per store
-  uint16_t *op = p.o + static_cast<int64_t>(q_begin) * p.o_tok + h * p.o_head;
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const float lt = l[qb] + xor32(l[qb]);
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    const int row = wq0 + qb * 32 + lq;
-    if (row >= Lq) continue;
-    uint16_t *orow = op + static_cast<int64_t>(row) * p.o_tok;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = db * 32 + 8 * g + 4 * hf;
-        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-        bf16x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = static_cast<__bf16>(o[qb][db][4 * g + e] * inv);
-        *reinterpret_cast<bf16x4 *>(orow + d) = v;
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Two waves per SIMD.  A workgroup of 8 waves owns 256 query rows (32 per
-// wave) of one (query sequence, head) pair, so every SIMD runs two waves
-// whose MFMA and softmax phases overlap; each wave stays within 256
-// registers.  K and V^T tiles of 64 keys are double-buffered in LDS with one
-// barrier per tile: waves 0-3 stage K rows (16-byte loads), waves 4-7 stage V
-// and transpose it in registers.  Global loads for tile t+2 are issued while
-// tile t is consumed.  Inside a tile the QK^T product of the second 32-key
-// block is issued before the softmax of the first.
-//
-// The softmax keeps its running maximum in log2 units and moves it only when
-// a new block exceeds it by more than kLazy (probabilities stay <= 2^kLazy,
-// far inside fp32 and bf16 range); O and the row sums are rescaled only
-// then.  The final O / l is the exact softmax either way.
-// ---------------------------------------------------------------------------
-constexpr int kWaves2 = 4;
-constexpr float kLazy = 8.0f;
-
-template <int D, int W>
-__global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
-  constexpr int BQ = 32 * W;
-  constexpr int HT = 32 * W;  // threads per staging role (half the workgroup)
-  constexpr int DS = D / 16;
-  constexpr int DB = D / 32;
-  constexpr int KS = D + 8;
-  constexpr int VS = kBK + 8;
-  constexpr int KCH = D / 8;
-  constexpr int KLD = kBK * KCH / HT;  // 16-byte K loads per thread of the K half
-  static_assert(KLD * HT == kBK * KCH, "K tile split");
-  constexpr int VGRP = kBK / 4;
-  constexpr int VPAIRS = VGRP * KCH;    // (4-key group, 16-byte chunk) pairs of the V half
-  constexpr int VPP = (VPAIRS + HT - 1) / HT;  // pairs per thread
-  static_assert(VPP * 4 <= 8 && KLD <= 8, "staging registers");
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VS];
+  constexpr int RS = D + 8;   // LDS row stride (elements) of K and V; +16 B spreads the banks
+  constexpr int KCH = D / 8;  // 16-byte chunks per row
+  constexpr int LD = kBK * KCH / kThreads;  // 16-byte loads per thread per tile, each of K and V
+  static_assert(LD * kThreads == kBK * KCH && LD <= 4, "tile split");
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBK * RS];
 
   const int wg = xcd_remap(blockIdx.x, p.n_wg);
   const int seq = wg / p.q_tiles, qt = wg % p.q_tiles;
@@ -356,6 +127,7 @@ __global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
   const int row_q = q0 + wave * 32 + lq;
   const float c = p.scale_log2;
 
+  // ---- Q^T operand, resident for the whole key loop
   bf16x8 qr[DS];
 #pragma unroll
   for (int s = 0; s < DS; ++s) {
@@ -370,88 +142,56 @@ __global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
     for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
   float m = -INFINITY, l = 0.0f;
 
-  // K/V reads go through buffer resources bounded at the sequence's last
-  // row: rows past Lk read as zero without a branch, and no access can leave
-  // the sequence.
-  const int64_t kv_bytes = static_cast<int64_t>(Lk) * p.kv_tok * 2;
-  const int nrec = static_cast<int>(kv_bytes < 0x7fffffff ? kv_bytes : 0x7fffffff);
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kp), 0, nrec, kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vp), 0, nrec, kRsrcWord3);
-  const int row_bytes = static_cast<int>(p.kv_tok) * 2;
-
-  // staging roles, decided per wave (readfirstlane makes the uniformity
-  // visible to the compiler, so each role keeps its own scalar resource)
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const bool k_loader = wave_u < W / 2;
-  const int vt = tid - HT;
-  uint4 st[8];
-
+  // ---- K/V staging through buffer resources based at the tile's first row
+  // and bounded at the sequence's last row: rows past Lk read as zero
+  // without a branch, no access can leave the sequence, and offsets stay
+  // within one tile whatever the sequence length
+  const int64_t row_elems = p.kv_tok;
+  const int row_bytes = static_cast<int>(row_elems) * 2;
+  uint4 sk[LD], sv[LD];
   auto load_tile = [&](int kt) {
-    const int kbase = kt * kBK;
-    if (k_loader) {
+    const int64_t first = static_cast<int64_t>(kt) * kBK;
+    const int64_t left = (static_cast<int64_t>(Lk) - first) * row_elems * 2;
+    const int nrec = static_cast<int>(left < 0x7fffffff ? left : 0x7fffffff);
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kp + first * row_elems), 0, nrec, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vp + first * row_elems), 0, nrec, kRsrcWord3);
 #pragma unroll
-      for (int r = 0; r < KLD; ++r) {
-        const int idx = tid + r * HT;
-        const int row = idx / KCH, ch = idx % KCH;
-        st[r] = bload16(rk, (kbase + row) * row_bytes + ch * 16);
-      }
-    } else {
-#pragma unroll
-      for (int pp = 0; pp < VPP; ++pp) {
-        const int pair = vt + pp * HT;
-        if (VPAIRS % HT == 0 || pair < VPAIRS) {
-          const int vgrp = pair % VGRP, vch = pair / VGRP;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) st[pp * 4 + j] = bload16(rv, (kbase + vgrp * 4 + j) * row_bytes + vch * 16);
-        }
-      }
+    for (int r = 0; r < LD; ++r) {
+      const int idx = tid + r * kThreads;
+      const int off = (idx / KCH) * row_bytes + (idx % KCH) * 16;
+      sk[r] = bload16(rk, off);
+      sv[r] = bload16(rv, off);
     }
   };
   auto store_tile = [&](int buf) {
-    if (k_loader) {
 #pragma unroll
-      for (int r = 0; r < KLD; ++r) {
-        const int idx = tid + r * HT;
-        const int row = idx / KCH, ch = idx % KCH;
-        *reinterpret_cast<uint4 *>(&Ks[buf][row * KS + ch * 8]) = st[r];
-      }
-    } else {
-#pragma unroll
-      for (int pp = 0; pp < VPP; ++pp) {
-        const int pair = vt + pp * HT;
-        if (VPAIRS % HT == 0 || pair < VPAIRS) {
-          const int vgrp = pair % VGRP, vch = pair / VGRP;
-          const uint4 *q4 = st + pp * 4;
-          const uint32_t w0[4] = {q4[0].x, q4[0].y, q4[0].z, q4[0].w};
-          const uint32_t w1[4] = {q4[1].x, q4[1].y, q4[1].z, q4[1].w};
-          const uint32_t w2[4] = {q4[2].x, q4[2].y, q4[2].z, q4[2].w};
-          const uint32_t w3[4] = {q4[3].x, q4[3].y, q4[3].z, q4[3].w};
-          const int col = vt_pos(vgrp * 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t lo01 = (w0[e] & 0xffffu) | (w1[e] << 16);
-            const uint32_t lo23 = (w2[e] & 0xffffu) | (w3[e] << 16);
-            const uint32_t hi01 = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
-            const uint32_t hi23 = (w2[e] >> 16) | (w3[e] & 0xffff0000u);
-            *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e) * VS + col]) = make_uint2(lo01, lo23);
-            *reinterpret_cast<uint2 *>(&Vt[buf][(vch * 8 + 2 * e + 1) * VS + col]) = make_uint2(hi01, hi23);
-          }
-        }
-      }
+    for (int r = 0; r < LD; ++r) {
+      const int idx = tid + r * kThreads;
+      const int e = (idx / KCH) * RS + (idx % KCH) * 8;
+      *reinterpret_cast<uint4 *>(&Ks[buf][e]) = sk[r];
+      *reinterpret_cast<uint4 *>(&Vs[buf][e]) = sv[r];
     }
   };
 
+  // S^T for the 32 keys kb*32.. of the tile in buf
   auto qk = [&](int buf, int kb) {
     f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
-      const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(&Ks[buf][(kb * 32 + lq) * KS + 16 * s + 8 * hf]));
+      const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4 *>(&Ks[buf][(kb * 32 + lq) * RS + 16 * s + 8 * hf]));
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qr[s], acc, 0, 0, 0);
     }
     return acc;
   };
+
+  // V^T fragment addresses: key row 4*hf + (lane%16)/4 (+8 for the second
+  // half of a 16-key step), dim column 16*((lane/16)%2) + 4*(lane%4)
+  const int v_row = 4 * hf + ((lane & 15) >> 2);
+  const int v_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   // softmax of one 64-key tile (two 32-key S^T blocks) and O^T += V^T P^T
   auto consume = [&](f32x16 s0, f32x16 s1, int buf, int kb0) {
@@ -479,8 +219,8 @@ __global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float sv = ks < 2 ? s0[8 * ks + j] : s1[8 * (ks - 2) + j];
-        const float e = __builtin_amdgcn_exp2f(fmaf(sv, c, -m));
+        const float sv_ = ks < 2 ? s0[8 * ks + j] : s1[8 * (ks - 2) + j];
+        const float e = __builtin_amdgcn_exp2f(fmaf(sv_, c, -m));
         ps += e;
         pb[ks][j] = static_cast<__bf16>(e);
       }
@@ -496,21 +236,21 @@ __global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const bf16x8 a =
-            as_bf16x8(*reinterpret_cast<const uint4 *>(&Vt[buf][(db * 32 + lq) * VS + 16 * ks + 8 * hf]));
+        const uint16_t *vptr = &Vs[buf][(16 * ks + v_row) * RS + db * 32 + v_col];
+        const i16x4 lo = lds_tr16(vptr), hi = lds_tr16(vptr + 8 * RS);
+        const i16x4 a8[2] = {lo, hi};
+        const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
       }
   };
 
   const int n_tiles = (Lk + kBK - 1) / kBK;
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-    if (n_tiles > 1) load_tile(1);
-  }
+  if (n_tiles > 0) load_tile(0);
+  if (n_tiles > 0) store_tile(0);
+  if (n_tiles > 1) load_tile(1);
   for (int kt = 0; kt < n_tiles; ++kt) {
     const int buf = kt & 1;
-    __syncthreads();
+    __syncthreads();  // tile kt visible; every wave is done with buffer buf^1
     if (kt + 1 < n_tiles) store_tile(buf ^ 1);
     if (kt + 2 < n_tiles) load_tile(kt + 2);
     const f32x16 s0 = qk(buf, 0);
@@ -518,6 +258,7 @@ __global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
     consume(s0, s1, buf, kt * kBK);
   }
 
+  // ---- epilogue: O = O^T / l, rows of 4 consecutive dims per store
   uint16_t *op = p.o + static_cast<int64_t>(q_begin) * p.o_tok + h * p.o_head;
   const float lt = half_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -538,29 +279,8 @@ __global__ void __launch_bounds__(64 * W, 2) attn_fwd2_kernel(AttnParams p) {
 }
 
 template <int D>
-static int launch_attn2(const pkv_attn_args *a, hipStream_t st) {
-  constexpr int BQ = 32 * kWaves2;
-  AttnParams p;
-  p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o;
-  p.cu_q = a->cu_seqlens_q; p.cu_k = a->cu_seqlens_k;
-  p.Hq = a->num_heads_q;
-  p.kv_per_head = a->kv_per_head;
-  p.q_tiles = (a->max_seqlen_q + BQ - 1) / BQ;
-  const int64_t n = static_cast<int64_t>(p.q_tiles) * a->num_batches * a->num_heads_q;
-  if (n > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: grid too large");
-  p.n_wg = static_cast<int>(n);
-  p.q_tok = a->q_tok_stride; p.q_head = a->q_head_stride;
-  p.kv_tok = a->kv_tok_stride; p.kv_head = a->kv_head_stride;
-  p.o_tok = a->o_tok_stride; p.o_head = a->o_head_stride;
-  p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
-  if (p.n_wg == 0) return PKV_OK;
-  hipLaunchKernelGGL((attn_fwd2_kernel<D, kWaves2>), dim3(p.n_wg), dim3(64 * kWaves2), 0, st, p);
-  return check_launch("attn_fwd2_kernel");
-}
-
-template <int D, int QB>
 static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
-  constexpr int BQ = 32 * QB * kAttnWaves;
+  constexpr int BQ = 32 * kWaves;
   AttnParams p;
   p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o;
   p.cu_q = a->cu_seqlens_q; p.cu_k = a->cu_seqlens_k;
@@ -575,7 +295,7 @@ static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   p.o_tok = a->o_tok_stride; p.o_head = a->o_head_stride;
   p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   if (p.n_wg == 0) return PKV_OK;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, QB>), dim3(p.n_wg), dim3(kAttnThreads), 0, st, p);
+  hipLaunchKernelGGL((attn_fwd_kernel<D>), dim3(p.n_wg), dim3(kThreads), 0, st, p);
   return check_launch("attn_fwd_kernel");
 }
 
@@ -594,10 +314,13 @@ extern "C" int pkv_ragged_attn_fwd(const pkv_attn_args *a, pkv_stream_t stream) 
   if ((a->q_tok_stride & align_mask) || (a->q_head_stride & align_mask) || (a->kv_tok_stride & align_mask) ||
       (a->kv_head_stride & align_mask) || (a->o_tok_stride & 3) || (a->o_head_stride & 3))
     return fail(PKV_ERR_INVALID, "ragged_attn: strides must keep 16-byte rows aligned");
+  // buffer offsets within one 64-row tile are 32-bit
+  if (a->kv_tok_stride * 2 * kBK > 0x7fffffff)
+    return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: kv token stride too large");
   hipStream_t st = as_stream(stream);
   switch (a->head_dim) {
-    case 128: return launch_attn2<128>(a, st);
-    case 64: return launch_attn2<64>(a, st);
+    case 128: return launch_attn<128>(a, st);
+    case 64: return launch_attn<64>(a, st);
     default: return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: head_dim %d (supported: 64, 128)", a->head_dim);
   }
 }
