@@ -253,8 +253,12 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
     __syncthreads();  // tile kt visible; every wave is done with buffer buf^1
     if (kt + 1 < n_tiles) store_tile(buf ^ 1);
     if (kt + 2 < n_tiles) load_tile(kt + 2);
+    // the QK^T MFMA cluster runs at raised wave priority, so a wave that
+    // reaches it issues ahead of its SIMD partner's softmax VALU work
+    __builtin_amdgcn_s_setprio(2);
     const f32x16 s0 = qk(buf, 0);
     const f32x16 s1 = qk(buf, 1);
+    __builtin_amdgcn_s_setprio(0);
     consume(s0, s1, buf, kt * kBK);
   }
 
