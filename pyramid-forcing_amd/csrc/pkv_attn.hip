@@ -148,8 +148,10 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
   // within one tile whatever the sequence length
   const int64_t row_elems = p.kv_tok;
   const int row_bytes = static_cast<int>(row_elems) * 2;
-  uint4 sk[LD], sv[LD];
-  auto load_tile = [&](int kt) {
+  // two register sets: tile t is loaded into set t%2 two iterations before
+  // it is stored, so each load has two tile-times to arrive
+  uint4 sk[2][LD], sv[2][LD];
+  auto load_tile = [&](int kt, uint4 (&k4)[LD], uint4 (&v4)[LD]) {
     const int64_t first = static_cast<int64_t>(kt) * kBK;
     const int64_t left = (static_cast<int64_t>(Lk) - first) * row_elems * 2;
     const int nrec = static_cast<int>(left < 0x7fffffff ? left : 0x7fffffff);
@@ -161,17 +163,17 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
     for (int r = 0; r < LD; ++r) {
       const int idx = tid + r * kThreads;
       const int off = (idx / KCH) * row_bytes + (idx % KCH) * 16;
-      sk[r] = bload16(rk, off);
-      sv[r] = bload16(rv, off);
+      k4[r] = bload16(rk, off);
+      v4[r] = bload16(rv, off);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf, const uint4 (&k4)[LD], const uint4 (&v4)[LD]) {
 #pragma unroll
     for (int r = 0; r < LD; ++r) {
       const int idx = tid + r * kThreads;
       const int e = (idx / KCH) * RS + (idx % KCH) * 8;
-      *reinterpret_cast<uint4 *>(&Ks[buf][e]) = sk[r];
-      *reinterpret_cast<uint4 *>(&Vs[buf][e]) = sv[r];
+      *reinterpret_cast<uint4 *>(&Ks[buf][e]) = k4[r];
+      *reinterpret_cast<uint4 *>(&Vs[buf][e]) = v4[r];
     }
   };
 
@@ -245,14 +247,20 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
   };
 
   const int n_tiles = (Lk + kBK - 1) / kBK;
-  if (n_tiles > 0) load_tile(0);
-  if (n_tiles > 0) store_tile(0);
-  if (n_tiles > 1) load_tile(1);
-  for (int kt = 0; kt < n_tiles; ++kt) {
+  if (n_tiles > 0) {
+    load_tile(0, sk[0], sv[0]);
+    store_tile(0, sk[0], sv[0]);
+  }
+  if (n_tiles > 1) load_tile(1, sk[1], sv[1]);
+  if (n_tiles > 2) load_tile(2, sk[0], sv[0]);
+  // iteration kt: tile kt is in LDS buffer kt%2; tile kt+1 (register set
+  // (kt+1)%2) is stored into the other buffer, then tile kt+3 is loaded into
+  // the set just freed
+  auto step = [&](int kt, uint4 (&k4)[LD], uint4 (&v4)[LD]) {
     const int buf = kt & 1;
     __syncthreads();  // tile kt visible; every wave is done with buffer buf^1
-    if (kt + 1 < n_tiles) store_tile(buf ^ 1);
-    if (kt + 2 < n_tiles) load_tile(kt + 2);
+    if (kt + 1 < n_tiles) store_tile(buf ^ 1, k4, v4);
+    if (kt + 3 < n_tiles) load_tile(kt + 3, k4, v4);
     // the QK^T MFMA cluster runs at raised wave priority, so a wave that
     // reaches it issues ahead of its SIMD partner's softmax VALU work
     __builtin_amdgcn_s_setprio(2);
@@ -260,6 +268,10 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
     const f32x16 s1 = qk(buf, 1);
     __builtin_amdgcn_s_setprio(0);
     consume(s0, s1, buf, kt * kBK);
+  };
+  for (int kt = 0; kt < n_tiles; kt += 2) {
+    step(kt, sk[1], sv[1]);
+    if (kt + 1 < n_tiles) step(kt + 1, sk[0], sv[0]);
   }
 
   // ---- epilogue: O = O^T / l, rows of 4 consecutive dims per store
