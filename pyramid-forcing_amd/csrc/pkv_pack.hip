@@ -214,6 +214,7 @@ __device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p
 // ---------------------------------------------------------------------------
 constexpr int kPackTok = 64;
 constexpr int kPackThreads = 256;
+constexpr int kPackPer = 4;  // 16-byte chunks per thread per round
 
 struct PackArgs {
   const uint16_t *k[4], *v[4];
@@ -252,18 +253,36 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     const bool rope = a.fuse && sp;
     const int64_t tr = rope ? a.tremap[seg] : -1;
     const int ntok = min(kPackTok, len - tok0);
-    for (int i = threadIdx.x; i < ntok * cpt; i += blockDim.x) {
-      const int tok = tok0 + i / cpt, ch = i % cpt;
-      const int64_t e = static_cast<int64_t>(tok) * a.D + ch * 8;
-      uint4 kk = ld16(sk + e);
-      const uint4 vv = ld16(sv + e);
-      if (rope) {
-        const int64_t *pp = sp + static_cast<int64_t>(tok) * 3;
-        const int64_t t = tr >= 0 ? tr : pp[0];
-        kk = rope_chunk(kk, ch, t, pp[1], pp[2], a.rope);
+    const int n_items = ntok * cpt;
+    // all of this thread's chunks of a round are loaded before any store
+    // (up to kPackPer 16-byte K and V reads in flight per thread; one round
+    // covers the tile for head_dim <= 128)
+    for (int base = 0; base < n_items; base += kPackPer * kPackThreads) {
+      uint4 kk[kPackPer], vv[kPackPer];
+#pragma unroll
+      for (int u = 0; u < kPackPer; ++u) {
+        const int i = base + threadIdx.x + u * kPackThreads;
+        if (i < n_items) {
+          const int64_t e = static_cast<int64_t>(tok0 + i / cpt) * a.D + (i % cpt) * 8;
+          kk[u] = ld16(sk + e);
+          vv[u] = ld16(sv + e);
+        }
       }
-      st16(ok + e, kk);
-      st16(ov + e, vv);
+#pragma unroll
+      for (int u = 0; u < kPackPer; ++u) {
+        const int i = base + threadIdx.x + u * kPackThreads;
+        if (i >= n_items) continue;
+        const int tok = tok0 + i / cpt, ch = i % cpt;
+        const int64_t e = static_cast<int64_t>(tok) * a.D + ch * 8;
+        uint4 k4 = kk[u];
+        if (rope) {
+          const int64_t *pp = sp + static_cast<int64_t>(tok) * 3;
+          const int64_t t = tr >= 0 ? tr : pp[0];
+          k4 = rope_chunk(k4, ch, t, pp[1], pp[2], a.rope);
+        }
+        st16(ok + e, k4);
+        st16(ov + e, vv[u]);
+      }
     }
     if (a.pos_out && sp) {
       int64_t *op = a.pos_out + dst * 3;

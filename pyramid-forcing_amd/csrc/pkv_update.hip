@@ -236,16 +236,21 @@ __global__ void route_kernel(HeadState *states, int H, int F, int64_t t0, int pa
   }
 }
 
-// grid = (ceil(FSEQ / kTokTile), H).  Order per thread and (token, chunk):
-// recent shift (ascending destination slot, which never overwrites a slot
-// before it was read), then each new frame to its sink or recent slot and,
-// for middle descriptors, to its middle slot.
-__global__ void scatter_kernel(FrameSrc src, PosSrc pos, PoolPtrs pools, Workspace ws, int layer,
-                               int H, int F, int FSEQ, int D, int max_sink, int max_middle,
-                               int max_recent) {
+// grid = (ceil(FSEQ / kScatTok), H), one thread per (token, 16-byte chunk).
+// Each thread first loads everything it will write (the recent slots the
+// FIFO shift moves and every new frame), then stores: the shift into
+// ascending slots, the new frames into their sink / recent slots and, for
+// middle descriptors, into their middle slots.  Loading before storing keeps
+// several 16-byte reads in flight per thread and makes the in-place shift
+// safe whatever slots the new frames land in.
+constexpr int kScatTok = 16;
+constexpr int kScatBatch = 4;  // frames (and shifted slots) staged per batch
+__global__ void __launch_bounds__(256) scatter_kernel(FrameSrc src, PosSrc pos, PoolPtrs pools, Workspace ws,
+                                                      int layer, int H, int F, int FSEQ, int D, int max_sink,
+                                                      int max_middle, int max_recent) {
   const int h = blockIdx.y;
   const Route r = ws.route[h];
-  const int tok0 = blockIdx.x * kTokTile;
+  const int tok0 = blockIdx.x * kScatTok;
   const int cpt = D / 8;
   const int64_t lh = static_cast<int64_t>(layer) * H + h;
   const int64_t slot_elems = static_cast<int64_t>(FSEQ) * D;
@@ -258,34 +263,58 @@ __global__ void scatter_kernel(FrameSrc src, PosSrc pos, PoolPtrs pools, Workspa
   const int32_t *dkind = ws.desc[0];
   const int32_t *dslot = ws.desc[1];
 
-  for (int i = threadIdx.x; i < kTokTile * cpt; i += blockDim.x) {
+  for (int i = threadIdx.x; i < kScatTok * cpt; i += blockDim.x) {
     const int tok = tok0 + i / cpt, c = (i % cpt) * 8;
     if (tok >= FSEQ) break;
     const int64_t e = static_cast<int64_t>(tok) * D + c;
-    for (int j = 0; j < r.keep; ++j) {
-      const uint4 kk = ld16(rec_k + (j + r.shift) * slot_elems + e);
-      const uint4 vv = ld16(rec_v + (j + r.shift) * slot_elems + e);
-      st16(rec_k + j * slot_elems + e, kk);
-      st16(rec_v + j * slot_elems + e, vv);
+    uint4 kk[kScatBatch], vv[kScatBatch];
+    // recent FIFO shift: slot j <- slot j + shift for j < keep (all sources
+    // of a batch read before its stores; batches ascend, and a slot written
+    // by one batch is never a source of a later batch since sources are
+    // >= shift > destinations of earlier batches)
+    for (int j0 = 0; j0 < r.keep; j0 += kScatBatch) {
+      const int n = min(kScatBatch, r.keep - j0);
+#pragma unroll
+      for (int b = 0; b < kScatBatch; ++b)
+        if (b < n) {
+          kk[b] = ld16(rec_k + (j0 + b + r.shift) * slot_elems + e);
+          vv[b] = ld16(rec_v + (j0 + b + r.shift) * slot_elems + e);
+        }
+#pragma unroll
+      for (int b = 0; b < kScatBatch; ++b)
+        if (b < n) {
+          st16(rec_k + (j0 + b) * slot_elems + e, kk[b]);
+          st16(rec_v + (j0 + b) * slot_elems + e, vv[b]);
+        }
     }
-    for (int f = 0; f < F; ++f) {
-      const int64_t so = src.off(f, h, tok) + c;
-      const uint4 kk = ld16(src.k + so);
-      const uint4 vv = ld16(src.v + so);
-      if (f < r.sink_writes) {
-        const int64_t s = r.sink_first + f;
-        st16(sink_k + s * slot_elems + e, kk);
-        st16(sink_v + s * slot_elems + e, vv);
-      } else {
-        const int64_t s = r.recent_first + (f - r.sink_writes);
-        st16(rec_k + s * slot_elems + e, kk);
-        st16(rec_v + s * slot_elems + e, vv);
-      }
-      if (dkind[h * F + f] == PKV_DST_MIDDLE) {
-        const int64_t s = dslot[h * F + f];
-        if (s >= 0 && s < max_middle) {
-          st16(mid_k + s * slot_elems + e, kk);
-          st16(mid_v + s * slot_elems + e, vv);
+    for (int f0 = 0; f0 < F; f0 += kScatBatch) {
+      const int n = min(kScatBatch, F - f0);
+#pragma unroll
+      for (int b = 0; b < kScatBatch; ++b)
+        if (b < n) {
+          const int64_t so = src.off(f0 + b, h, tok) + c;
+          kk[b] = ld16(src.k + so);
+          vv[b] = ld16(src.v + so);
+        }
+#pragma unroll
+      for (int b = 0; b < kScatBatch; ++b) {
+        if (b >= n) continue;
+        const int f = f0 + b;
+        if (f < r.sink_writes) {
+          const int64_t s = r.sink_first + f;
+          st16(sink_k + s * slot_elems + e, kk[b]);
+          st16(sink_v + s * slot_elems + e, vv[b]);
+        } else {
+          const int64_t s = r.recent_first + (f - r.sink_writes);
+          st16(rec_k + s * slot_elems + e, kk[b]);
+          st16(rec_v + s * slot_elems + e, vv[b]);
+        }
+        if (dkind[h * F + f] == PKV_DST_MIDDLE) {
+          const int64_t s = dslot[h * F + f];
+          if (s >= 0 && s < max_middle) {
+            st16(mid_k + s * slot_elems + e, kk[b]);
+            st16(mid_v + s * slot_elems + e, vv[b]);
+          }
         }
       }
     }
@@ -293,7 +322,7 @@ __global__ void scatter_kernel(FrameSrc src, PosSrc pos, PoolPtrs pools, Workspa
 
   // positions: one thread per token of the tile
   const int t = threadIdx.x;
-  if (t < kTokTile && tok0 + t < FSEQ) {
+  if (t < kScatTok && tok0 + t < FSEQ) {
     const int tok = tok0 + t;
     const int64_t pe = static_cast<int64_t>(tok) * 3;
     const int64_t pslot = static_cast<int64_t>(FSEQ) * 3;
@@ -390,76 +419,131 @@ struct MergeArgs {
 };
 
 // Stable CSR of gid[0..FSEQ) over groups [0, ng): gstart (exclusive prefix
-// of the counts) and members (tokens of each group in ascending order).
-// Wave 0 places the tokens 64 at a time; the rank of a token among equal
-// group ids of its 64-token chunk comes from a match mask built with one
-// ballot per bit of the group id.
-__device__ void build_csr(const int32_t *gid, int FSEQ, int ng, int32_t *cnt, int32_t *gstart, int32_t *members) {
-  const int tid = threadIdx.x;
-  for (int g = tid; g < ng; g += blockDim.x) cnt[g] = 0;
+// of the counts) and members (tokens of each group in ascending order),
+// built by all four waves.  Wave w owns a contiguous quarter of the tokens
+// and walks it in 64-token chunks; inside a chunk the tokens sharing a group
+// id are found with one ballot per bit of the id (the match mask), so the
+// rank of a token among its group's tokens of the chunk is a popcount and
+// the highest such lane alone updates the per-(wave, group) counter.
+// Pass 1 counts, a block-wide scan turns the counts into per-(wave, group)
+// bases (quarters in order), pass 2 places the tokens.
+constexpr int kMergeWaves = kMergeThreads / 64;
+
+__device__ inline uint64_t group_match(int g, bool valid, int bits) {
+  uint64_t match = __ballot(valid);
+  for (int b = 0; b < bits; ++b) {
+    const uint64_t ones = __ballot(valid && ((g >> b) & 1));
+    match &= ((g >> b) & 1) ? ones : ~ones;
+  }
+  return match;
+}
+
+__device__ void build_csr(const int32_t *gid, int FSEQ, int ng, int32_t *cntw, int32_t *gstart, int32_t *members,
+                          int32_t *part) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < kMergeWaves * ng; i += blockDim.x) cntw[i] = 0;
+  int bits = 1;
+  while ((1 << bits) < ng) ++bits;
+  const int quarter = ((FSEQ + kMergeWaves * 64 - 1) / (kMergeWaves * 64)) * 64;
+  const int t_begin = wave * quarter, t_end = min(FSEQ, t_begin + quarter);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int32_t *mycnt = cntw + wave * ng;
   __syncthreads();
-  for (int t = tid; t < FSEQ; t += blockDim.x) atomicAdd(&cnt[gid[t]], 1);
-  __syncthreads();
-  if (tid == 0) {
-    int32_t acc = 0;
-    for (int g = 0; g < ng; ++g) {
-      gstart[g] = acc;
-      acc += cnt[g];
-      cnt[g] = 0;  // reused as the running fill count
-    }
-    gstart[ng] = acc;
+  // pass 1: counts per (wave, group)
+  for (int c0 = t_begin; c0 < t_end; c0 += 64) {
+    const int t = c0 + lane;
+    const bool valid = t < t_end;
+    const int g = valid ? gid[t] : 0;
+    const uint64_t match = group_match(g, valid, bits);
+    if (valid && (match >> lane) == 1ull) mycnt[g] += __popcll(match);
+    // LDS accesses of one wave execute in program order: the next chunk
+    // sees these updates without a barrier
   }
   __syncthreads();
-  if (tid < 64) {
-    int bits = 1;
-    while ((1 << bits) < ng) ++bits;
-    const uint64_t below = (tid == 0) ? 0ull : (~0ull >> (64 - tid));
-    for (int c0 = 0; c0 < FSEQ; c0 += 64) {
-      const int t = c0 + tid;
-      const bool valid = t < FSEQ;
-      const int g = valid ? gid[t] : -1;
-      uint64_t match = __ballot(valid);
-      for (int b = 0; b < bits; ++b) {
-        const uint64_t ones = __ballot(valid && ((g >> b) & 1));
-        match &= ((g >> b) & 1) ? ones : ~ones;
-      }
-      if (valid) {
-        const int rank = __popcll(match & below);
-        const int base = cnt[g];
-        members[gstart[g] + base + rank] = t;
-        // the highest lane of each group advances its fill count
-        if ((match >> tid) == 1ull) cnt[g] = base + __popcll(match);
-      }
-      // LDS accesses of one wave execute in program order, so the next
-      // chunk sees this chunk's count updates without a barrier
+  // scan: gstart[g] = sum of all counts of groups < g; cntw[w][g] becomes the
+  // base of wave w's tokens of group g
+  const int per = (ng + blockDim.x - 1) / blockDim.x;
+  const int g0 = tid * per, g1 = min(ng, g0 + per);
+  int32_t acc = 0;
+  for (int g = g0; g < g1; ++g)
+    for (int w = 0; w < kMergeWaves; ++w) acc += cntw[w * ng + g];
+  part[tid] = acc;
+  __syncthreads();
+  for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {
+    const int32_t v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int32_t base = part[tid] - acc;
+  for (int g = g0; g < g1; ++g) {
+    gstart[g] = base;
+    for (int w = 0; w < kMergeWaves; ++w) {
+      const int32_t c = cntw[w * ng + g];
+      cntw[w * ng + g] = base;
+      base += c;
+    }
+  }
+  if (tid == static_cast<int>(blockDim.x) - 1) gstart[ng] = part[tid];
+  __syncthreads();
+  // pass 2: placement
+  for (int c0 = t_begin; c0 < t_end; c0 += 64) {
+    const int t = c0 + lane;
+    const bool valid = t < t_end;
+    const int g = valid ? gid[t] : 0;
+    const uint64_t match = group_match(g, valid, bits);
+    if (valid) {
+      const int b = mycnt[g];
+      members[b + __popcll(match & below)] = t;
+      if ((match >> lane) == 1ull) mycnt[g] = b + __popcll(match);
     }
   }
   __syncthreads();
 }
 
+constexpr int kMaxMergeFrames = 64;
+constexpr int kMaxMergeSlots = 8;
+
+// One workgroup per head, frames in order.  All descriptors and running
+// weight sums are read in one round trip; the group lists built for a block
+// stay in LDS for the later frames of that block in the same call.
 __global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) {
   extern __shared__ int32_t smem[];
-  int32_t *gid = smem;                          // [FSEQ]
-  int32_t *members = gid + a.FSEQ;              // [FSEQ]
-  int32_t *gstart = members + a.FSEQ;           // [kMaxMergeGroups + 1]
-  int32_t *cnt = gstart + kMaxMergeGroups + 1;  // [kMaxMergeGroups]
+  int32_t *gid = smem;                                    // [FSEQ]
+  int32_t *members = gid + a.FSEQ;                        // [FSEQ]
+  int32_t *gstart = members + a.FSEQ;                     // [kMaxMergeGroups + 1]
+  int32_t *cntw = gstart + kMaxMergeGroups + 1;           // [kMergeWaves * kMaxMergeGroups]
+  int32_t *part = cntw + kMergeWaves * kMaxMergeGroups;   // [kMergeThreads]
+  __shared__ int32_t s_desc[kMaxMergeFrames][4];
+  __shared__ float s_wsum[kMaxMergeSlots];
+  __shared__ int32_t s_ng[kMaxMergeSlots];
   __shared__ int32_t s_maxy, s_maxx;
   const int h = blockIdx.x;
   const int tid = threadIdx.x;
   const int MTPA = a.MTPA;
   const int32_t bf = a.states[h].block_frames;
   const int32_t patch = a.states[h].patch_size;
-
+  if (tid < a.F) {
+    const int di = h * a.F + tid;
+    s_desc[tid][0] = a.desc_kind[di];
+    s_desc[tid][1] = a.desc_slot[di];
+    s_desc[tid][2] = a.desc_new[di];
+    s_desc[tid][3] = a.desc_fin[di];
+  }
+  if (tid < a.MMA) {
+    const int64_t hs = static_cast<int64_t>(h) * a.MMA + tid;
+    s_wsum[tid] = a.ml.accum_weight_sum ? a.ml.accum_weight_sum[hs] : 0.0f;
+    s_ng[tid] = a.ml.accum_num_groups[hs];
+  }
+  __syncthreads();
+  int csr_slot = -1;  // slot whose group lists are in LDS
+  int ng = 0;
   for (int f = 0; f < a.F; ++f) {
     const int di = h * a.F + f;
-    const int kind = a.desc_kind[di];
-    const int slot = a.desc_slot[di];
+    const int kind = s_desc[f][0], slot = s_desc[f][1], is_new = s_desc[f][2], fin = s_desc[f][3];
     if (kind != PKV_DST_MERGE_ACCUM || slot < 0 || slot >= a.MMA) continue;
-    const int is_new = a.desc_new[di];
-    const int fin = a.desc_fin[di];
     const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
     int32_t *gids_g = a.ml.accum_group_ids + hs * a.FSEQ;
-    int ng;
     if (is_new) {
       if (tid == 0) { s_maxy = -1; s_maxx = -1; }
       __syncthreads();
@@ -497,19 +581,23 @@ __global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) 
       }
       if (tid == 0) {
         a.ml.accum_num_groups[hs] = ng;
+        s_ng[slot] = ng;
+        s_wsum[slot] = 0.0f;
         if (a.ml.accum_weight_sum) a.ml.accum_weight_sum[hs] = 0.0f;
       }
-    } else {
-      ng = a.ml.accum_num_groups[hs];
-      if (ng > MTPA) ng = MTPA;
-      for (int t = tid; t < a.FSEQ; t += blockDim.x) gid[t] = gids_g[t];
-    }
-    __syncthreads();
-    build_csr(gid, a.FSEQ, ng, cnt, gstart, members);
-    if (is_new) {
+      __syncthreads();
+      build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
+      csr_slot = slot;
       float *tpg = a.ml.accum_tokens_per_group + hs * MTPA;
       for (int g = tid; g < MTPA; g += blockDim.x)
         tpg[g] = g < ng ? static_cast<float>(gstart[g + 1] - gstart[g]) * static_cast<float>(bf) : 0.0f;
+    } else if (csr_slot != slot) {
+      ng = s_ng[slot];
+      if (ng > MTPA) ng = MTPA;
+      for (int t = tid; t < a.FSEQ; t += blockDim.x) gid[t] = gids_g[t];
+      __syncthreads();
+      build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
+      csr_slot = slot;
     }
     // per-frame snapshot for the accumulation launch
     int32_t *wm = a.ws.members + static_cast<int64_t>(di) * a.FSEQ;
@@ -520,7 +608,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) 
       a.ws.ng[di] = ng;
       float ws = 1.0f;
       if (a.weights && a.ml.accum_weight_sum) {
-        ws = a.ml.accum_weight_sum[hs] + a.weights[f];
+        ws = s_wsum[slot] + a.weights[f];
+        s_wsum[slot] = ws;
         a.ml.accum_weight_sum[hs] = ws;
       }
       a.ws.wsum[di] = ws;
@@ -629,7 +718,16 @@ static int launch_merge(const MergeArgs &ma, hipStream_t st) {
   if (ma.MTPA > kMaxMergeGroups)
     return fail(PKV_ERR_UNSUPPORTED, "merge_accum: %d tokens per anchor exceed %d", ma.MTPA, kMaxMergeGroups);
   if (ma.D % 8 != 0) return fail(PKV_ERR_INVALID, "merge_accum: head_dim %d not a multiple of 8", ma.D);
-  const size_t smem = (2 * static_cast<size_t>(ma.FSEQ) + 2 * kMaxMergeGroups + 1) * sizeof(int32_t);
+  if (ma.F > kMaxMergeFrames)
+    return fail(PKV_ERR_UNSUPPORTED, "merge_accum: %d frames per call exceed %d", ma.F, kMaxMergeFrames);
+  if (ma.MMA > kMaxMergeSlots)
+    return fail(PKV_ERR_UNSUPPORTED, "merge_accum: %d active merge blocks exceed %d", ma.MMA, kMaxMergeSlots);
+  const size_t smem = (2 * static_cast<size_t>(ma.FSEQ) + (1 + kMergeWaves) * kMaxMergeGroups + 1 + kMergeThreads) *
+                      sizeof(int32_t);
+  if (smem > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void *>(merge_prep_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
+    return fail(PKV_ERR_HIP, "merge_accum: cannot reserve %zu bytes of LDS", smem);
   hipLaunchKernelGGL(merge_prep_kernel, dim3(ma.H), dim3(kMergeThreads), smem, st, ma);
   int rc = check_launch("merge_prep_kernel");
   if (rc) return rc;
@@ -767,7 +865,7 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   if ((rc = check_launch("route_kernel"))) return rc;
   FrameSrc src{a->new_k, a->new_v, static_cast<int64_t>(FSEQ) * a->tok_stride, a->head_stride, a->tok_stride};
   PosSrc pos{nullptr, a->t0, a->spatial_width, H, FSEQ};
-  dim3 grid((FSEQ + kTokTile - 1) / kTokTile, H);
+  dim3 grid((FSEQ + kScatTok - 1) / kScatTok, H);
   hipLaunchKernelGGL(scatter_kernel, grid, dim3(256), 0, st, src, pos, pool_ptrs(geo, pools), ws, a->layer,
                      H, a->frames, FSEQ, D, geo->max_sink, geo->max_middle, geo->max_recent);
   if ((rc = check_launch("scatter_kernel"))) return rc;

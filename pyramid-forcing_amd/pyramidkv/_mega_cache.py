@@ -50,6 +50,8 @@ class MegaCacheCtx:
     spatial_width: int = 52
     spatial_height: int = 30
     has_merge_head: bool = False
+    # per layer: any Veil (merge) head; layers without one skip the merge launches
+    layer_has_merge: list = field(default_factory=list)
     sink_caps_per_head: torch.Tensor = None
     committed_vc: torch.Tensor = None
     freqs: torch.Tensor = None
@@ -108,7 +110,7 @@ class MegaCache:
             nk = nk.contiguous()
         _ops.ops().cache_update(ctx.mgr, ctx.states_bytes[l], ctx.sink_caps_per_head[l], ctx.committed_vc[l], nk, nv,
                                 l, t0, 1 if clean else 0, 1 if pending == t0 else 0, ctx.spatial_width,
-                                bool(ctx.has_merge_head))
+                                bool(ctx.layer_has_merge[l] if ctx.layer_has_merge else ctx.has_merge_head))
         ctx.pending_block[l] = None if clean else t0
 
     def last_update_descriptors(self, frames: int):
@@ -235,11 +237,13 @@ def build_mega_caches(num_layers: int, num_heads: int, head_dim: int, frame_seql
     states_np = np.zeros((num_layers, num_heads), dtype=_mega_state_ops.PER_HEAD_STATE_DTYPE)
     sink_caps = np.zeros((num_layers, num_heads), dtype=np.int64)
     any_merge = False
+    layer_merge = []
     for l in range(num_layers):
         if len(compositions[l]) != num_heads:
             raise ValueError(f"compositions[{l}] has {len(compositions[l])} heads, expected {num_heads}")
         per_head = [_composition_to_perhead_state(c) for c in compositions[l]]
-        any_merge = any_merge or any(s.kind == ref.SK_MERGE for s in per_head)
+        layer_merge.append(any(s.kind == ref.SK_MERGE for s in per_head))
+        any_merge = any_merge or layer_merge[-1]
         for h, s in enumerate(per_head):
             sink_caps[l, h] = int(s.sink_capacity)
         states_np[l] = _mega_state_ops.pack_states(per_head)
@@ -258,7 +262,7 @@ def build_mega_caches(num_layers: int, num_heads: int, head_dim: int, frame_seql
                        history_time_mapping_mode=history_time_mapping_mode,
                        history_relative_t_max=history_relative_t_max,
                        history_time_soft_factor=history_time_soft_factor, spatial_width=spatial_width,
-                       spatial_height=spatial_height, has_merge_head=any_merge,
+                       spatial_height=spatial_height, has_merge_head=any_merge, layer_has_merge=layer_merge,
                        sink_caps_per_head=torch.from_numpy(sink_caps).to(device=device).contiguous(), freqs=freqs,
                        freq_parts=freq_parts, freq_parts_flat=freq_parts_flat,
                        pending_block=[None] * num_layers)
