@@ -45,8 +45,9 @@ struct PlanParams {
 // recent -> middle (Wave bucket of the current phase, or the Anchor/lag
 // ring in slot order) -> merge anchors (mega_plan.cc:133-264).  Offsets are
 // relative to the pair; the caller adds the pair's global base.
+template <bool kWrite>
 __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int64_t *vc_h,
-                             const int32_t *mtc_h, int c, int h, int base, const pkv_plan_out &o) {
+                             const int32_t *mtc_h, int c, int h, int base, int32_t dst0, const pkv_plan_out &o) {
   const int S = p.S;
   const int64_t t_c = p.t[c], sync_t = p.sync_t[c];
   const int thresh = s.sink_capacity;
@@ -54,13 +55,15 @@ __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int6
   int32_t run = 0;
   int fp = 0;
   auto put = [&](int kind, int sg, int len, int64_t traw, int64_t tremap) {
-    const int i = base + fp;
-    o.src_kind[i] = kind;
-    o.src_slot_global[i] = sg;
-    o.seg_lengths[i] = len;
-    o.dst_token_offsets[i] = run;
-    o.anchor_t_raw[i] = traw;
-    o.anchor_t_remap[i] = tremap;
+    if (kWrite) {
+      const int i = base + fp;
+      o.src_kind[i] = kind;
+      o.src_slot_global[i] = sg;
+      o.seg_lengths[i] = len;
+      o.dst_token_offsets[i] = dst0 + run;
+      o.anchor_t_raw[i] = traw;
+      o.anchor_t_remap[i] = tremap;
+    }
     run += len;
     ++fp;
   };
@@ -104,7 +107,7 @@ __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int6
       put(PKV_SEG_MERGE, p.slot_off[3] + h * p.MMB + slot, tok, 0, s.merge_completed_median_t[i]);
     }
   }
-  for (int i = fp; i < S; ++i) {
+  for (int i = fp; kWrite && i < S; ++i) {
     const int j = base + i;
     o.src_kind[j] = PKV_SEG_INACTIVE;
     o.src_slot_global[j] = 0;
@@ -116,16 +119,39 @@ __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int6
   return run;
 }
 
+// One workgroup.  The layer's state records, counters and merge token counts
+// are staged in LDS with coalesced reads (when they fit), a count-only pass
+// gives every (chunk, head) pair its token total, a block-wide exclusive scan
+// turns those into offsets, and a second pass emits each pair's segments
+// with final destination offsets.
+constexpr int kPlanStageHeads = 48;  // heads whose records are staged in LDS
+
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const HeadState *states,
                                                             const int64_t *vc, const int32_t *mtc,
                                                             pkv_plan_out o, int32_t *total_out) {
   __shared__ int32_t len[kMaxPlanPairs];
   __shared__ int32_t part[kPlanThreads];
+  __shared__ __attribute__((aligned(16))) HeadState s_states[kPlanStageHeads];
+  __shared__ int64_t s_vc[kPlanStageHeads * 3];
+  __shared__ int32_t s_mtc[kPlanStageHeads * kMaxMergeBlocks];
   const int tid = threadIdx.x;
   const int pairs = p.C * p.H;
+  const bool staged = p.H <= kPlanStageHeads && p.MMB <= kMaxMergeBlocks;
+  if (staged) {
+    const int words = p.H * static_cast<int>(sizeof(HeadState)) / 4;
+    const int32_t *src = reinterpret_cast<const int32_t *>(states);
+    int32_t *dst = reinterpret_cast<int32_t *>(s_states);
+    for (int i = tid; i < words; i += blockDim.x) dst[i] = src[i];
+    for (int i = tid; i < p.H * 3; i += blockDim.x) s_vc[i] = vc[i];
+    for (int i = tid; i < p.H * p.MMB; i += blockDim.x) s_mtc[i] = mtc[i];
+  }
+  __syncthreads();
+  const HeadState *st = staged ? s_states : states;
+  const int64_t *vcs = staged ? s_vc : vc;
+  const int32_t *mts = staged ? s_mtc : mtc;
   for (int q = tid; q < pairs; q += blockDim.x) {
     const int c = q / p.H, h = q % p.H;
-    len[q] = emit_pair(p, states[h], vc + h * 3, mtc + h * p.MMB, c, h, q * p.S, o);
+    len[q] = emit_pair<false>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, 0, o);
   }
   __syncthreads();
   // exclusive scan of len[0..pairs): contiguous chunk per thread, then a
@@ -151,13 +177,10 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
   __syncthreads();
   if (tid == 0) o.cu_seqlens_k[0] = 0;
   for (int q = tid; q < pairs; q += blockDim.x) {
+    const int c = q / p.H, h = q % p.H;
     const int32_t b = len[q];
-    for (int i = 0; i < p.S; ++i) {
-      const int j = q * p.S + i;
-      if (o.src_kind[j] >= 0) o.dst_token_offsets[j] += b;
-    }
-    const int32_t end = (q + 1 < pairs) ? len[q + 1] : part[kPlanThreads - 1];
-    o.cu_seqlens_k[q + 1] = end;
+    const int32_t n = emit_pair<true>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, b, o);
+    o.cu_seqlens_k[q + 1] = b + n;
   }
   if (tid == 0 && total_out) *total_out = part[kPlanThreads - 1];
 }

@@ -171,12 +171,38 @@ __host__ __device__ inline Workspace carve_workspace(void *base, int H, int F) {
 // the same tail slots, so a pass that finds the shift already applied
 // (shift_pending) only rewrites the tail.  That reproduces the reference's
 // snapshot-and-restore contents without copying the recent pool.
-__global__ void route_kernel(HeadState *states, int H, int F, int64_t t0, int pass_kind,
-                             int shift_pending, int max_sink, int max_recent,
-                             const int64_t *sink_caps, int64_t *committed_vc, int64_t *vc,
-                             Workspace ws) {
-  const int h = blockIdx.x * blockDim.x + threadIdx.x;
-  if (h >= H) return;
+// A workgroup covers kRouteHeads heads; their state records are copied into
+// LDS with coalesced 4-byte accesses, updated there by one thread per head,
+// and copied back.
+constexpr int kRouteHeads = 64;
+constexpr int kRouteThreads = 256;
+__device__ void route_head(HeadState &s, int h, int F, int64_t t0, int pass_kind, int shift_pending, int max_sink,
+                           int max_recent, const int64_t *sink_caps, int64_t *committed_vc, int64_t *vc,
+                           const Workspace &ws);
+
+__global__ void __launch_bounds__(kRouteThreads) route_kernel(HeadState *states, int H, int F, int64_t t0,
+                                                              int pass_kind, int shift_pending, int max_sink,
+                                                              int max_recent, const int64_t *sink_caps,
+                                                              int64_t *committed_vc, int64_t *vc, Workspace ws) {
+  __shared__ __attribute__((aligned(16))) HeadState s_st[kRouteHeads];
+  const int h0 = blockIdx.x * kRouteHeads;
+  const int nh = min(kRouteHeads, H - h0);
+  const int words = nh * static_cast<int>(sizeof(HeadState)) / 4;
+  int32_t *g = reinterpret_cast<int32_t *>(states + h0);
+  int32_t *l = reinterpret_cast<int32_t *>(s_st);
+  for (int i = threadIdx.x; i < words; i += blockDim.x) l[i] = g[i];
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < nh)
+    route_head(s_st[threadIdx.x], h0 + threadIdx.x, F, t0, pass_kind, shift_pending, max_sink, max_recent, sink_caps,
+               committed_vc, vc, ws);
+  __syncthreads();
+  if (pass_kind == 1)
+    for (int i = threadIdx.x; i < words; i += blockDim.x) g[i] = l[i];
+}
+
+__device__ void route_head(HeadState &s, int h, int F, int64_t t0, int pass_kind, int shift_pending, int max_sink,
+                           int max_recent, const int64_t *sink_caps, int64_t *committed_vc, int64_t *vc,
+                           const Workspace &ws) {
   const int64_t sc = committed_vc[h * 3 + 0];
   const int64_t mc = committed_vc[h * 3 + 1];
   const int64_t rc = committed_vc[h * 3 + 2];
@@ -223,7 +249,6 @@ __global__ void route_kernel(HeadState *states, int H, int F, int64_t t0, int pa
   out.merge_local_idx = ws.desc[5];
   out.merge_finalize_completed_idx = ws.desc[6];
   out.merge_is_new_block = ws.desc[7];
-  HeadState &s = states[h];
   for (int f = 0; f < F; ++f) {
     FrameDesc d = skip_desc();
     if (pass_kind == 1) d = sm_step(s, static_cast<int32_t>(t0 + f));
@@ -376,7 +401,7 @@ __global__ void __launch_bounds__(256) scatter_kernel(FrameSrc src, PosSrc pos, 
 // groups of its head, zeroes them on a new block, adds the frame's tokens
 // in ascending order (one fp32 add per token, the reference's accumulation
 // sequence) and writes bf16(sum * (1 / divisor)) on finalize.
-constexpr int kGroupsPerWg = 32;
+constexpr int kGroupsPerWg = 16;
 constexpr int kMergeThreads = 256;
 constexpr int kMaxMergeFseq = 8192;
 constexpr int kMaxMergeGroups = 1024;
@@ -629,70 +654,155 @@ __global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) 
   }
 }
 
+// Workgroup = (range of kGroupsPerWg groups, head); thread = (group, 8-wide
+// dim chunk), so every accumulator element has one owner thread for all
+// frames.  The member lists of the workgroup's groups for every merge frame
+// are staged in LDS first; each thread keeps its accumulators in registers
+// across the frames of a slot, loads a batch of member tokens before adding
+// them (ascending token order, frames in descriptor order: the reference's
+// fp32 addition sequence) and stores the accumulators when the slot changes
+// and at the end.
+constexpr int kAccMembersLds = 4096;  // staged member ids per workgroup
+constexpr int kAccBatch = 8;          // member tokens loaded per batch
+
 __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a) {
+  __shared__ int32_t s_desc[kMaxMergeFrames][4];
+  __shared__ int32_t s_ng[kMaxMergeFrames];
+  __shared__ float s_wsum[kMaxMergeFrames];
+  __shared__ int32_t s_gs[kMaxMergeFrames][kGroupsPerWg + 1];  // member-slice offsets (relative to s_off)
+  __shared__ int32_t s_off[kMaxMergeFrames];
+  __shared__ int32_t s_mem[kAccMembersLds];
+  __shared__ int32_t s_nmerge, s_staged;
   const int h = blockIdx.y;
   const int g0 = blockIdx.x * kGroupsPerWg;
   const int tid = threadIdx.x;
   const int D = a.D, MTPA = a.MTPA;
   const int cpt = D / 8;
   const int32_t bf = a.states[h].block_frames;
-  for (int f = 0; f < a.F; ++f) {
-    const int di = h * a.F + f;
-    const int kind = a.desc_kind[di];
-    const int slot = a.desc_slot[di];
-    if (kind != PKV_DST_MERGE_ACCUM || slot < 0 || slot >= a.MMA) continue;
-    const int is_new = a.desc_new[di];
-    const int fin = a.desc_fin[di];
-    const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
-    float *sum_k = a.ml.accum_sum_k + hs * MTPA * D;
-    float *sum_v = a.ml.accum_sum_v + hs * MTPA * D;
-    const int32_t *members = a.ws.members + static_cast<int64_t>(di) * a.FSEQ;
-    const int32_t *gstart = a.ws.gstart + static_cast<int64_t>(di) * (MTPA + 1);
-    const int ng = a.ws.ng[di];
-    const float w = a.weights ? a.weights[f] : 1.0f;
-    // thread = (group, 8-wide dim chunk); the mapping is the same for every
-    // frame, so each accumulator element has a single owner thread
-    for (int i = tid; i < kGroupsPerWg * cpt; i += blockDim.x) {
-      const int g = g0 + i / cpt, c = (i % cpt) * 8;
-      if (g >= MTPA) break;
-      float *pk = sum_k + static_cast<int64_t>(g) * D + c;
-      float *pv = sum_v + static_cast<int64_t>(g) * D + c;
-      float ak[8], av[8];
-      if (is_new) {
-        for (int e = 0; e < 8; ++e) { ak[e] = 0.0f; av[e] = 0.0f; }
-      } else {
-        for (int e = 0; e < 8; ++e) { ak[e] = pk[e]; av[e] = pv[e]; }
+  if (tid < a.F) {
+    const int di = h * a.F + tid;
+    const int kind = a.desc_kind[di], slot = a.desc_slot[di];
+    const bool merge = kind == PKV_DST_MERGE_ACCUM && slot >= 0 && slot < a.MMA;
+    s_desc[tid][0] = merge ? 1 : 0;
+    s_desc[tid][1] = slot;
+    s_desc[tid][2] = a.desc_new[di];
+    s_desc[tid][3] = a.desc_fin[di];
+    s_ng[tid] = merge ? a.ws.ng[di] : 0;
+    s_wsum[tid] = merge ? a.ws.wsum[di] : 1.0f;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int n = 0;
+    for (int f = 0; f < a.F; ++f) n += s_desc[f][0];
+    s_nmerge = n;
+  }
+  __syncthreads();
+  if (s_nmerge == 0) return;
+  // group-range offsets of every merge frame (gstart is read from the
+  // frame's snapshot) and the total member count they span
+  if (tid < a.F && s_desc[tid][0]) {
+    const int f = tid;
+    const int32_t *gstart = a.ws.gstart + static_cast<int64_t>(h * a.F + f) * (MTPA + 1);
+    const int ng = s_ng[f];
+    const int lo = min(g0, ng), hi = min(g0 + kGroupsPerWg, ng);
+    const int32_t base = gstart[lo];
+    for (int j = 0; j <= kGroupsPerWg; ++j) s_gs[f][j] = gstart[min(lo + j, hi)] - base;
+    s_off[f] = base;  // absolute start of the slice in the frame's member list
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int total = 0;
+    for (int f = 0; f < a.F; ++f)
+      if (s_desc[f][0]) total += s_gs[f][kGroupsPerWg];
+    s_staged = total <= kAccMembersLds;
+  }
+  __syncthreads();
+  const bool staged = s_staged;
+  if (staged) {
+    int pos = 0;
+    for (int f = 0; f < a.F; ++f) {
+      if (!s_desc[f][0]) continue;
+      const int n = s_gs[f][kGroupsPerWg];
+      const int32_t *mem = a.ws.members + static_cast<int64_t>(h * a.F + f) * a.FSEQ + s_off[f];
+      for (int i = tid; i < n; i += blockDim.x) s_mem[pos + i] = mem[i];
+      pos += n;
+    }
+  }
+  __syncthreads();
+
+  for (int it = tid; it < kGroupsPerWg * cpt; it += blockDim.x) {
+    const int gl = it / cpt, c = (it % cpt) * 8;
+    const int g = g0 + gl;
+    if (g >= MTPA) break;
+    float ak[8], av[8];
+    int cur = -1;  // slot whose accumulators are in registers
+    int pos = 0;   // start of the current frame's staged members
+    for (int f = 0; f < a.F; ++f) {
+      if (!s_desc[f][0]) continue;
+      const int slot = s_desc[f][1], is_new = s_desc[f][2], fin = s_desc[f][3];
+      const int ng = s_ng[f];
+      const int fpos = pos;
+      pos += s_gs[f][kGroupsPerWg];
+      const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
+      if (slot != cur) {
+        if (cur >= 0) {
+          const int64_t ho = static_cast<int64_t>(h) * a.MMA + cur;
+          float *pk = a.ml.accum_sum_k + (ho * MTPA + g) * D + c;
+          float *pv = a.ml.accum_sum_v + (ho * MTPA + g) * D + c;
+          for (int e = 0; e < 8; ++e) { pk[e] = ak[e]; pv[e] = av[e]; }
+        }
+        cur = slot;
+        if (!is_new) {
+          const float *pk = a.ml.accum_sum_k + (hs * MTPA + g) * D + c;
+          const float *pv = a.ml.accum_sum_v + (hs * MTPA + g) * D + c;
+          for (int e = 0; e < 8; ++e) { ak[e] = pk[e]; av[e] = pv[e]; }
+        }
       }
+      if (is_new)
+        for (int e = 0; e < 8; ++e) { ak[e] = 0.0f; av[e] = 0.0f; }
+      const float w = a.weights ? a.weights[f] : 1.0f;
       if (g < ng) {
-        for (int m = gstart[g]; m < gstart[g + 1]; ++m) {
-          const int64_t so = a.src.off(f, h, members[m]) + c;
-          const uint4 kk = ld16(a.src.k + so);
-          const uint4 vv = ld16(a.src.v + so);
-          const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
-          const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-          for (int e = 0; e < 4; ++e) {
-            const float k0 = bf16_to_f32(static_cast<uint16_t>(kw[e] & 0xffff));
-            const float k1 = bf16_to_f32(static_cast<uint16_t>(kw[e] >> 16));
-            const float v0 = bf16_to_f32(static_cast<uint16_t>(vw[e] & 0xffff));
-            const float v1 = bf16_to_f32(static_cast<uint16_t>(vw[e] >> 16));
-            if (a.weights) {
-              ak[2 * e] = __fadd_rn(ak[2 * e], __fmul_rn(w, k0));
-              ak[2 * e + 1] = __fadd_rn(ak[2 * e + 1], __fmul_rn(w, k1));
-              av[2 * e] = __fadd_rn(av[2 * e], __fmul_rn(w, v0));
-              av[2 * e + 1] = __fadd_rn(av[2 * e + 1], __fmul_rn(w, v1));
-            } else {
-              ak[2 * e] += k0;
-              ak[2 * e + 1] += k1;
-              av[2 * e] += v0;
-              av[2 * e + 1] += v1;
+        const int m0 = s_gs[f][gl], m1 = s_gs[f][gl + 1];
+        const int32_t *gmem = a.ws.members + static_cast<int64_t>(h * a.F + f) * a.FSEQ + s_off[f];
+        for (int mb = m0; mb < m1; mb += kAccBatch) {
+          const int n = min(kAccBatch, m1 - mb);
+          uint4 kk[kAccBatch], vv[kAccBatch];
+#pragma unroll
+          for (int b = 0; b < kAccBatch; ++b)
+            if (b < n) {
+              const int tok = staged ? s_mem[fpos + mb + b] : gmem[mb + b];
+              const int64_t so = a.src.off(f, h, tok) + c;
+              kk[b] = ld16(a.src.k + so);
+              vv[b] = ld16(a.src.v + so);
+            }
+#pragma unroll
+          for (int b = 0; b < kAccBatch; ++b) {
+            if (b >= n) continue;
+            const uint32_t kw[4] = {kk[b].x, kk[b].y, kk[b].z, kk[b].w};
+            const uint32_t vw[4] = {vv[b].x, vv[b].y, vv[b].z, vv[b].w};
+            for (int e = 0; e < 4; ++e) {
+              const float k0 = bf16_to_f32(static_cast<uint16_t>(kw[e] & 0xffff));
+              const float k1 = bf16_to_f32(static_cast<uint16_t>(kw[e] >> 16));
+              const float v0 = bf16_to_f32(static_cast<uint16_t>(vw[e] & 0xffff));
+              const float v1 = bf16_to_f32(static_cast<uint16_t>(vw[e] >> 16));
+              if (a.weights) {
+                ak[2 * e] = __fadd_rn(ak[2 * e], __fmul_rn(w, k0));
+                ak[2 * e + 1] = __fadd_rn(ak[2 * e + 1], __fmul_rn(w, k1));
+                av[2 * e] = __fadd_rn(av[2 * e], __fmul_rn(w, v0));
+                av[2 * e + 1] = __fadd_rn(av[2 * e + 1], __fmul_rn(w, v1));
+              } else {
+                ak[2 * e] += k0;
+                ak[2 * e + 1] += k1;
+                av[2 * e] += v0;
+                av[2 * e + 1] += v1;
+              }
             }
           }
         }
       }
-      for (int e = 0; e < 8; ++e) { pk[e] = ak[e]; pv[e] = av[e]; }
       if (fin >= 0 && fin < a.MMB && g < ng) {
-        const int32_t count = gstart[g + 1] - gstart[g];
-        const float div = a.weights ? static_cast<float>(count) * a.ws.wsum[di]
+        const int32_t count = s_gs[f][gl + 1] - s_gs[f][gl];
+        const float div = a.weights ? static_cast<float>(count) * s_wsum[f]
                                     : static_cast<float>(count) * static_cast<float>(bf);
         const float inv = div > 0.0f ? 1.0f / div : 0.0f;
         const int64_t hp = static_cast<int64_t>(h) * a.MMB + fin;
@@ -708,6 +818,12 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
         st16(a.ml.merge_k + (hp * MTPA + g) * D + c, ok);
         st16(a.ml.merge_v + (hp * MTPA + g) * D + c, ov);
       }
+    }
+    if (cur >= 0) {
+      const int64_t ho = static_cast<int64_t>(h) * a.MMA + cur;
+      float *pk = a.ml.accum_sum_k + (ho * MTPA + g) * D + c;
+      float *pv = a.ml.accum_sum_v + (ho * MTPA + g) * D + c;
+      for (int e = 0; e < 8; ++e) { pk[e] = ak[e]; pv[e] = av[e]; }
     }
   }
 }
@@ -858,7 +974,7 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   hipStream_t st = as_stream(stream);
   Workspace ws = carve_workspace(a->workspace, H, a->frames);
   int64_t *vc = pools->valid_count + static_cast<int64_t>(a->layer) * H * 3;
-  hipLaunchKernelGGL(route_kernel, dim3((H + 63) / 64), dim3(64), 0, st,
+  hipLaunchKernelGGL(route_kernel, dim3((H + kRouteHeads - 1) / kRouteHeads), dim3(kRouteThreads), 0, st,
                      reinterpret_cast<HeadState *>(a->states_layer), H, a->frames, a->t0, a->pass_kind,
                      a->shift_pending, geo->max_sink, geo->max_recent, a->sink_caps_layer,
                      a->committed_vc_layer, vc, ws);
