@@ -231,6 +231,13 @@ __device__ inline uint4 rope_chunk(uint4 raw, int chunk, int64_t t, int64_t y, i
 
 __device__ inline uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 __device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
+// streaming store (non-temporal): the flat K/V of one layer call is larger
+// than the caches, so its lines are not kept
+__device__ inline void st16_nt(uint16_t *p, uint4 v) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
+}
 
 // ---------------------------------------------------------------------------
 // pack
@@ -303,8 +310,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
           const int64_t t = tr >= 0 ? tr : pp[0];
           k4 = rope_chunk(k4, ch, t, pp[1], pp[2], a.rope);
         }
-        st16(ok + e, k4);
-        st16(ov + e, vv[u]);
+        st16_nt(ok + e, k4);
+        st16_nt(ov + e, vv[u]);
       }
     }
     if (a.pos_out && sp) {
