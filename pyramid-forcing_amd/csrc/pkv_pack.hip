@@ -468,7 +468,7 @@ int pkv_pack(const pkv_geometry *geo, const pkv_pools *pools, const int32_t *src
   a.tiles_per_seg = (seg_max + kPackTok - 1) / kPackTok;
   const int64_t items = static_cast<int64_t>(n_segments) * a.tiles_per_seg;
   if (items > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "pyramidkv_pack: too many segments");
-  const int grid = static_cast<int>(items < 4096 ? items : 4096);
+  const int grid = static_cast<int>(items);  // one workgroup per (segment, tile); inactive ones exit at once
   hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kPackThreads), 0, as_stream(stream), a);
   return check_launch("pack_kernel");
 }
