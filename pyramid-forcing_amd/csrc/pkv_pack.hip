@@ -31,7 +31,7 @@ __host__ __device__ inline int64_t map_sink_time(int64_t t, int mode, int cmin, 
 }
 
 constexpr int kMaxPlanChunks = 64;
-constexpr int kPlanThreads = 256;
+constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanPairs = 4096;
 
 struct PlanParams {
@@ -41,81 +41,130 @@ struct PlanParams {
   int64_t sync_t[kMaxPlanChunks];
 };
 
-// Segment emission for one (chunk c, head h), in the reference order sink ->
-// recent -> middle (Wave bucket of the current phase, or the Anchor/lag
-// ring in slot order) -> merge anchors (mega_plan.cc:133-264).  Offsets are
-// relative to the pair; the caller adds the pair's global base.
+// Segment emission for one (chunk c, head h) by one wave, in the reference
+// order sink -> recent -> middle (Wave bucket of the current phase, or the
+// Anchor/lag ring in slot order) -> merge anchors (mega_plan.cc:133-264).
+// Every lane evaluates one candidate segment of that fixed order; a
+// candidate's position is the number of valid candidates before it (ballot
+// popcount), positions >= S are dropped (the reference stops appending at
+// S), and the destination offsets are a wave prefix sum of the lengths.
+// Returns the pair's token total (uniform over the wave).
+__device__ inline int32_t wave_incl_sum(int32_t x, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
 template <bool kWrite>
-__device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int64_t *vc_h,
-                             const int32_t *mtc_h, int c, int h, int base, int32_t dst0, const pkv_plan_out &o) {
+__device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int64_t *vc_h, const int32_t *mtc_h,
+                             int c, int h, int base, int32_t dst0, const pkv_plan_out &o) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int S = p.S;
   const int64_t t_c = p.t[c], sync_t = p.sync_t[c];
   const int thresh = s.sink_capacity;
-  const int recent_min_t = 0x7fffffff;
-  int32_t run = 0;
+  const int32_t recent_min_t = 0x7fffffff;
+  const int n_sink_raw = static_cast<int>(vc_h[0]);
+  const int n_sink = (thresh > 0 && thresh < n_sink_raw) ? thresh : n_sink_raw;
+  const int n_recent = static_cast<int>(vc_h[2]);
+  const int kind_s = s.kind;
+  const int period = s.period > 0 ? s.period : 1;
+  const int bucket_cap = s.bucket_cap > 0 ? s.bucket_cap : 1;
+  const int phase = static_cast<int>(((t_c % period) + period) % period);
+  const int b0 = phase * kMaxBucket;
+  const int b1 = b0 + (bucket_cap < kMaxBucket ? bucket_cap : kMaxBucket);
+  const int tc = s.tkey_count;
+  const int mcc = s.merge_completed_count;
+  const int c_sink = p.max_sink, c_rec = c_sink + p.max_recent, c_mid = c_rec + kMaxTKeyed,
+            n_cand = c_mid + kMaxMergeBlocks;
   int fp = 0;
-  auto put = [&](int kind, int sg, int len, int64_t traw, int64_t tremap) {
-    if (kWrite) {
-      const int i = base + fp;
+  int32_t run = 0;
+  for (int j0 = 0; j0 < n_cand; j0 += 64) {
+    const int j = j0 + lane;
+    bool valid = false;
+    int kind = PKV_SEG_INACTIVE, sg = 0, len = 0;
+    int64_t traw = -1, tremap = -1;
+    if (j < c_sink) {
+      valid = j < n_sink;
+      kind = PKV_SEG_SINK;
+      sg = p.slot_off[0] + h * p.max_sink + j;
+      len = p.FSEQ;
+      traw = j;
+      tremap = sync_t;
+    } else if (j < c_rec) {
+      const int r = j - c_sink;
+      valid = r < n_recent;
+      kind = PKV_SEG_RECENT;
+      sg = p.slot_off[2] + h * p.max_recent + r;
+      len = p.FSEQ;
+    } else if (j < c_mid) {
+      const int i = j - c_rec;
+      kind = PKV_SEG_MIDDLE;
+      len = p.FSEQ;
+      if (kind_s == SK_CYCLIC) {
+        const int idx = b0 + i;
+        if (idx < b1 && idx < kMaxPhase * kMaxBucket) {
+          const int32_t t = s.cyclic_t[idx];
+          valid = s.cyclic_slot[idx] >= 0 && t >= thresh && t < recent_min_t;
+          sg = p.slot_off[1] + h * p.max_middle + idx;
+          traw = t;
+          tremap = sync_t;
+        }
+      } else if (kind_s == SK_STRIDE || kind_s == SK_LAG) {
+        if (i < tc) {
+          const int32_t t = s.tkey_t[i];
+          valid = t >= thresh && t < recent_min_t;
+          sg = p.slot_off[1] + h * p.max_middle + i;
+          traw = t;
+          tremap = kind_s == SK_STRIDE ? sync_t : -1;
+        }
+      }
+    } else if (j < n_cand) {
+      const int i = j - c_mid;
+      if (kind_s == SK_MERGE && i < mcc) {
+        const int slot = s.merge_completed_slot[i];
+        if (slot >= 0 && slot < p.MMB && s.merge_completed_start_t[i] > 0 &&
+            s.merge_completed_end_t[i] < recent_min_t) {
+          const int32_t tok = mtc_h[slot];
+          valid = tok > 0;
+          kind = PKV_SEG_MERGE;
+          sg = p.slot_off[3] + h * p.MMB + slot;
+          len = tok;
+          traw = 0;
+          tremap = s.merge_completed_median_t[i];
+        }
+      }
+    }
+    const uint64_t mask = __ballot(valid);
+    const int pos = fp + __popcll(mask & below);
+    const bool emit = valid && pos < S;
+    const int32_t l = emit ? len : 0;
+    const int32_t incl = wave_incl_sum(l, lane);
+    if (kWrite && emit) {
+      const int i = base + pos;
       o.src_kind[i] = kind;
       o.src_slot_global[i] = sg;
       o.seg_lengths[i] = len;
-      o.dst_token_offsets[i] = dst0 + run;
+      o.dst_token_offsets[i] = dst0 + run + incl - l;
       o.anchor_t_raw[i] = traw;
       o.anchor_t_remap[i] = tremap;
     }
-    run += len;
-    ++fp;
-  };
-  const int n_sink_raw = static_cast<int>(vc_h[0]);
-  const int n_sink = (thresh > 0 && thresh < n_sink_raw) ? thresh : n_sink_raw;
-  for (int q = 0; q < n_sink && q < p.max_sink; ++q) put(PKV_SEG_SINK, p.slot_off[0] + h * p.max_sink + q, p.FSEQ, q, sync_t);
-  const int n_recent = static_cast<int>(vc_h[2]);
-  for (int r = 0; r < n_recent && r < p.max_recent; ++r) put(PKV_SEG_RECENT, p.slot_off[2] + h * p.max_recent + r, p.FSEQ, -1, -1);
-  if (s.kind == SK_CYCLIC) {
-    const int period = s.period > 0 ? s.period : 1;
-    const int bucket_cap = s.bucket_cap > 0 ? s.bucket_cap : 1;
-    const int phase = static_cast<int>(((t_c % period) + period) % period);
-    const int b0 = phase * kMaxBucket;
-    const int b1 = b0 + (bucket_cap < kMaxBucket ? bucket_cap : kMaxBucket);
-    for (int i = b0; i < b1 && i < kMaxPhase * kMaxBucket; ++i) {
-      if (s.cyclic_slot[i] < 0) continue;
-      if (s.cyclic_t[i] < thresh) continue;
-      if (s.cyclic_t[i] >= recent_min_t) continue;
-      put(PKV_SEG_MIDDLE, p.slot_off[1] + h * p.max_middle + i, p.FSEQ, s.cyclic_t[i], sync_t);
-      if (fp >= S) break;
-    }
-  } else if (s.kind == SK_STRIDE || s.kind == SK_LAG) {
-    const int tc = s.tkey_count;
-    for (int i = 0; i < tc && i < kMaxTKeyed; ++i) {
-      if (s.tkey_t[i] < thresh) continue;
-      if (s.tkey_t[i] >= recent_min_t) continue;
-      put(PKV_SEG_MIDDLE, p.slot_off[1] + h * p.max_middle + i, p.FSEQ, s.tkey_t[i], s.kind == SK_STRIDE ? sync_t : -1);
-      if (fp >= S) break;
-    }
+    run += __shfl(incl, 63);
+    fp = min(S, fp + __popcll(mask));
   }
-  if (s.kind == SK_MERGE) {
-    const int mcc = s.merge_completed_count;
-    for (int i = 0; i < mcc && i < kMaxMergeBlocks; ++i) {
-      const int slot = s.merge_completed_slot[i];
-      if (slot < 0 || slot >= p.MMB) continue;
-      if (s.merge_completed_start_t[i] <= 0) continue;
-      if (s.merge_completed_end_t[i] >= recent_min_t) continue;
-      const int32_t tok = mtc_h[slot];
-      if (tok <= 0) continue;
-      if (fp >= S) break;
-      put(PKV_SEG_MERGE, p.slot_off[3] + h * p.MMB + slot, tok, 0, s.merge_completed_median_t[i]);
+  if (kWrite)
+    for (int i = fp + lane; i < S; i += 64) {
+      const int jj = base + i;
+      o.src_kind[jj] = PKV_SEG_INACTIVE;
+      o.src_slot_global[jj] = 0;
+      o.seg_lengths[jj] = 0;
+      o.dst_token_offsets[jj] = 0;
+      o.anchor_t_raw[jj] = -1;
+      o.anchor_t_remap[jj] = -1;
     }
-  }
-  for (int i = fp; kWrite && i < S; ++i) {
-    const int j = base + i;
-    o.src_kind[j] = PKV_SEG_INACTIVE;
-    o.src_slot_global[j] = 0;
-    o.seg_lengths[j] = 0;
-    o.dst_token_offsets[j] = 0;
-    o.anchor_t_raw[j] = -1;
-    o.anchor_t_remap[j] = -1;
-  }
   return run;
 }
 
@@ -149,9 +198,11 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
   const HeadState *st = staged ? s_states : states;
   const int64_t *vcs = staged ? s_vc : vc;
   const int32_t *mts = staged ? s_mtc : mtc;
-  for (int q = tid; q < pairs; q += blockDim.x) {
+  const int wave = tid >> 6, n_waves = blockDim.x >> 6;
+  for (int q = wave; q < pairs; q += n_waves) {
     const int c = q / p.H, h = q % p.H;
-    len[q] = emit_pair<false>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, 0, o);
+    const int32_t n = emit_pair<false>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, 0, o);
+    if ((tid & 63) == 0) len[q] = n;
   }
   __syncthreads();
   // exclusive scan of len[0..pairs): contiguous chunk per thread, then a
@@ -176,11 +227,11 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
   }
   __syncthreads();
   if (tid == 0) o.cu_seqlens_k[0] = 0;
-  for (int q = tid; q < pairs; q += blockDim.x) {
+  for (int q = wave; q < pairs; q += n_waves) {
     const int c = q / p.H, h = q % p.H;
     const int32_t b = len[q];
     const int32_t n = emit_pair<true>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, b, o);
-    o.cu_seqlens_k[q + 1] = b + n;
+    if ((tid & 63) == 0) o.cu_seqlens_k[q + 1] = b + n;
   }
   if (tid == 0 && total_out) *total_out = part[kPlanThreads - 1];
 }
