@@ -24,6 +24,11 @@
  *   pkv_plan_multi           mega_plan.cc:286-407, 513-654  (mega_plan / mega_plan_multi)
  *   pkv_pack                 pyramidkv_pack.cu:189-311      (launch_pyramidkv_pack)
  *   pkv_plan_pack            _mega_cache.py:461-523 (plan -> layer offset -> pack of attend)
+ *   pkv_scatter_copy         scatter_copy.cu:13-47, scatter_copy_bind.cpp:451-465 (scatter_copy)
+ *   pkv_pos_override         scatter_copy.cu:53-71, scatter_copy_bind.cpp:467-479 (apply_pos_override)
+ *   pkv_refresh_readout      scatter_copy.cu:77-168, scatter_copy_bind.cpp:527-627 (refresh_readout_layout)
+ *   pkv_anchor_store_write_frames  scatter_copy.cu:170-225, scatter_copy_bind.cpp:629-683
+ *   pkv_plan_legacy          pyramidkv_plan.cc:46-133 (pyramidkv_plan)
  *   pkv_rope_apply           rope.py:18-68, triton_rope.py:17-247 (apply_rope_to_flat_k)
  *   pkv_ragged_attn_fwd      _mega_cache.py:540-559, flash_attn_varlen_func (flash-attn 2.8.3)
  *   pkv_cache_update         _mega_cache.py:136-414 (MegaCache.update: sink/recent routing,
@@ -218,6 +223,58 @@ int pkv_plan_pack(const pkv_geometry *geo, const pkv_pools *pools,
                   const int64_t *current_t_list, int32_t num_chunks,
                   const pkv_remap *remap, const pkv_rope_tables *rope,
                   const pkv_plan_out *plan_ws, pkv_stream_t stream);
+
+/* scatter_copy: segment i copies lengths[i] rows of row_bytes bytes from
+ * the device address src_ptrs[i] to dst rows offsets[i].. (all int64 device
+ * arrays).  Segments whose rows fall outside [0, dst_rows) are skipped. */
+int pkv_scatter_copy(const int64_t *src_ptrs, const int64_t *lengths,
+                     const int64_t *offsets, int32_t n_segments, void *dst,
+                     int64_t dst_rows, int64_t row_bytes, pkv_stream_t stream);
+
+/* apply_pos_override: pos[i, 0] = vals[r] for starts[r] <= i < ends[r]
+ * (pos [rows, 3] int64; ranges clipped to [0, rows)). */
+int pkv_pos_override(int64_t *pos, int64_t rows, const int64_t *starts,
+                     const int64_t *ends, const int64_t *vals, int32_t n_ranges,
+                     pkv_stream_t stream);
+
+/* refresh_readout_layout: per segment, copy lengths[i] rows of K and V from
+ * the device addresses src_ptrs_k/v[i] to dst rows offsets[i].., and write
+ * dst_pos / dst_frame_ids from the int64 [len, 3] positions at
+ * src_ptrs_pos[i]: flags bit 2 sets t = dynamic_rope_t[i]; otherwise bit 0
+ * applies the history time map (mode 0 none, 1 relative_clamp, 2
+ * relative_softcap) relative to current_t; bit 1 makes the frame id the
+ * source t instead of the written t.  Segments outside [0, dst_rows) are
+ * skipped. */
+typedef struct pkv_refresh_args {
+  const int64_t *src_ptrs_k, *src_ptrs_v, *src_ptrs_pos;
+  const int64_t *offsets, *lengths, *flags, *dynamic_rope_t;
+  void *dst_k, *dst_v;
+  int64_t *dst_pos, *dst_frame_ids;
+  int64_t dst_rows, row_bytes, current_t, history_relative_t_max;
+  int32_t n_segments, history_mode_code;
+  float history_soft_factor;
+} pkv_refresh_args;
+int pkv_refresh_readout(const pkv_refresh_args *args, pkv_stream_t stream);
+
+/* anchor_store_write_frames: frame_desc [n, 2] int64 (source frame, store
+ * slot); copies a frame of frame_seqlen rows of K, V (row_bytes each) and
+ * its [frame_seqlen, 3] int64 positions into the slot.  Descriptors with a
+ * negative field, a source frame >= src_frames or a slot >= capacity are
+ * skipped. */
+int pkv_anchor_store_write_frames(const void *k_seq, const void *v_seq,
+                                  const int64_t *pos_seq, int64_t src_frames,
+                                  const int64_t *frame_desc, int32_t n_frames,
+                                  void *store_k, void *store_v, int64_t *store_pos,
+                                  int64_t capacity, int64_t frame_seqlen,
+                                  int64_t row_bytes, pkv_stream_t stream);
+
+/* pyramidkv_plan (legacy): over all L*H heads, three segments each in the
+ * order sink, recent, middle covering slots 0..valid_count-1; outputs cu
+ * [L*H+1] and [3*L*H] descriptor arrays (int32, device). */
+int pkv_plan_legacy(const pkv_geometry *geo, const int64_t *valid_count,
+                    int32_t *cu_seqlens_k, int32_t *src_kind,
+                    int32_t *src_slot_global, int32_t *seg_lengths,
+                    int32_t *dst_token_offsets, pkv_stream_t stream);
 
 /* apply_rope_to_flat_k: out[n, D] = rot(k[n, D], pos[n, 3]); out may equal k. */
 int pkv_rope_apply(const uint16_t *k, const int64_t *pos, int64_t n_tokens,

@@ -504,3 +504,99 @@ class MegaCacheRef:
         k, v, p = pack(self.pools(), g, sk, sga, sl, dst, tremap, self.tables)
         return dict(cu=cu, sk=sk, sg=sg, sl=sl, dst=dst, traw=traw, tremap=tremap, total=total, k=k[:total],
                     v=v[:total], pos=p[:total])
+
+
+# ---------------------------------------------------------------------------
+# data-movement ops (pyramidkv/csrc/scatter_copy.cu) and the legacy planner
+# (pyramidkv/csrc/pyramidkv_plan.cc)
+# ---------------------------------------------------------------------------
+def scatter_copy(srcs, lengths, offsets, dst: np.ndarray) -> None:
+    """scatter_copy.cu:13-47: segment i copies lengths[i] rows of srcs[i]
+    (row-major, same columns as dst) to dst rows offsets[i]..; dst mutated."""
+    for s, n, o in zip(srcs, lengths, offsets):
+        n, o = int(n), int(o)
+        if n <= 0:
+            continue
+        dst[o:o + n] = np.asarray(s).reshape(-1, *dst.shape[1:])[:n]
+
+
+def pos_override(pos: np.ndarray, starts, ends, vals) -> None:
+    """scatter_copy.cu:53-71: pos[i, 0] = val for start <= i < end."""
+    for s, e, v in zip(starts, ends, vals):
+        pos[int(s):int(e), 0] = int(v)
+
+
+def map_history_t(src_t: int, current_t: int, mode: int, rel_max: int, soft: float) -> int:
+    """scatter_copy.cu:142-160: mode 0 keeps t, 1 clamps the relative time
+    at rel_max, 2 compresses the excess by `soft` with round-half-to-even on
+    the float32 product; the result is clamped at 0."""
+    rel = max(0, current_t - src_t)
+    mapped = src_t
+    if mode == 1:
+        mapped = current_t - min(rel, rel_max)
+    elif mode == 2:
+        if rel > rel_max:
+            rel = rel_max + int(np.rint(np.float32(rel - rel_max) * np.float32(soft)))
+        mapped = current_t - rel
+    return max(0, mapped)
+
+
+_HIST_CODES = {"none": 0, "relative_clamp": 1, "relative_softcap": 2}
+
+
+def refresh_readout(src_k, src_v, src_pos, offsets, lengths, flags, rope_t, dst_k, dst_v, dst_pos, dst_frame,
+                    current_t: int, mode: str, rel_max: int, soft: float) -> None:
+    """scatter_copy.cu:77-168 (all outputs mutated): flags bit 2 overrides
+    t with rope_t, else bit 0 applies the history map; bit 1 makes the frame
+    id the source t."""
+    code = _HIST_CODES.get(mode, 0)
+    for i, (o, n) in enumerate(zip(offsets, lengths)):
+        o, n, f = int(o), int(n), int(flags[i])
+        if n <= 0:
+            continue
+        dst_k[o:o + n] = src_k[i][:n]
+        dst_v[o:o + n] = src_v[i][:n]
+        for r in range(n):
+            t0 = int(src_pos[i][r, 0])
+            t = t0
+            if f & 4:
+                t = int(rope_t[i])
+            elif (f & 1) and rel_max > 0:
+                t = map_history_t(t0, current_t, code, rel_max, soft)
+            dst_pos[o + r] = (t, src_pos[i][r, 1], src_pos[i][r, 2])
+            dst_frame[o + r] = t0 if (f & 2) else t
+
+
+def write_frames(k_seq, v_seq, pos_seq, frame_desc, store_k, store_v, store_pos) -> None:
+    """scatter_copy.cu:170-225: frame (src, slot) -> store slot (stores mutated)."""
+    fs = store_k.shape[1]
+    for src, slot in np.asarray(frame_desc).reshape(-1, 2):
+        src, slot = int(src), int(slot)
+        if src < 0 or slot < 0:
+            continue
+        store_k[slot] = k_seq[src * fs:(src + 1) * fs]
+        store_v[slot] = v_seq[src * fs:(src + 1) * fs]
+        store_pos[slot] = pos_seq[src * fs:(src + 1) * fs]
+
+
+def plan_legacy(vc: np.ndarray, fseq: int, max_sink: int, max_middle: int, max_recent: int):
+    """pyramidkv_plan.cc:46-133: per (layer, head) the segments sink, recent,
+    middle over slots 0..valid_count-1; returns (cu, sk, sg, sl, dst)."""
+    L, H, _ = vc.shape
+    n = L * H
+    slots = {0: max_sink, 1: max_middle, 2: max_recent}
+    cu = np.zeros(n + 1, np.int32)
+    sk = np.full(3 * n, -1, np.int32)
+    sg, sl, dst = (np.zeros(3 * n, np.int32) for _ in range(3))
+    run = 0
+    for q in range(n):
+        l, h = divmod(q, H)
+        for kp, kind in enumerate((0, 2, 1)):
+            d = q * 3 + kp
+            v = int(vc[l, h, kind])
+            if v <= 0:
+                continue
+            sk[d], sg[d], sl[d], dst[d] = kind, q * slots[kind], v * fseq, run
+            run += v * fseq
+        cu[q + 1] = run
+    return cu, sk, sg, sl, dst

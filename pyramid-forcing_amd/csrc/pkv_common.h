@@ -95,6 +95,8 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
 void set_error(const char *fmt, ...);
 int fail(int status, const char *fmt, ...);
 int check_launch(const char *what);
+// PKV_OK or PKV_ERR_INVALID with a message for a malformed geometry
+int check_geometry(const pkv_geometry *g);
 
 inline hipStream_t as_stream(pkv_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 

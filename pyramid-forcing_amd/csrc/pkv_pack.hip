@@ -319,13 +319,15 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     const int kind = a.kind[seg];
     if (kind < 0 || kind > 3) continue;
     const int len = a.len[seg];
-    const int tok0 = tile * kPackTok;
-    if (len <= 0 || tok0 >= len) continue;
+    if (len <= 0 || tile * kPackTok >= len) continue;
     const int64_t sg = a.sg[seg];
     const int64_t dst = a.dst[seg];
-    if (sg < 0 || sg >= a.slots[kind] || dst < 0 || dst + len > a.capacity || !a.k[kind]) continue;
     const int stride = (kind == PKV_SEG_MERGE) ? a.MTPA : a.FSEQ;
-    if (len > stride) continue;
+    // a segment starts at its slot and may run on through the following
+    // slots of the pool (the legacy plan's whole-pool segments), never past
+    // the pool's end
+    if (sg < 0 || sg * stride + len > a.slots[kind] * stride || dst < 0 || dst + len > a.capacity || !a.k[kind])
+      continue;
     const uint16_t *sk = a.k[kind] + sg * stride * a.D;
     const uint16_t *sv = a.v[kind] + sg * stride * a.D;
     const int64_t *sp = a.pos[kind] ? a.pos[kind] + sg * stride * 3 : nullptr;
@@ -333,45 +335,49 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     uint16_t *ov = a.v_out + dst * a.D;
     const bool rope = a.fuse && sp;
     const int64_t tr = rope ? a.tremap[seg] : -1;
-    const int ntok = min(kPackTok, len - tok0);
-    const int n_items = ntok * cpt;
-    // all of this thread's chunks of a round are loaded before any store
-    // (up to kPackPer 16-byte K and V reads in flight per thread; one round
-    // covers the tile for head_dim <= 128)
-    for (int base = 0; base < n_items; base += kPackPer * kPackThreads) {
-      uint4 kk[kPackPer], vv[kPackPer];
+    // segments up to tiles_per_seg tiles long (every frame or merge anchor)
+    // take one pass; longer ones are walked tiles_per_seg tiles at a time
+    for (int tok0 = tile * kPackTok; tok0 < len; tok0 += a.tiles_per_seg * kPackTok) {
+      const int ntok = min(kPackTok, len - tok0);
+      const int n_items = ntok * cpt;
+      // all of this thread's chunks of a round are loaded before any store
+      // (up to kPackPer 16-byte K and V reads in flight per thread; one round
+      // covers the tile for head_dim <= 128)
+      for (int base = 0; base < n_items; base += kPackPer * kPackThreads) {
+        uint4 kk[kPackPer], vv[kPackPer];
 #pragma unroll
-      for (int u = 0; u < kPackPer; ++u) {
-        const int i = base + threadIdx.x + u * kPackThreads;
-        if (i < n_items) {
-          const int64_t e = static_cast<int64_t>(tok0 + i / cpt) * a.D + (i % cpt) * 8;
-          kk[u] = ld16(sk + e);
-          vv[u] = ld16(sv + e);
+        for (int u = 0; u < kPackPer; ++u) {
+          const int i = base + threadIdx.x + u * kPackThreads;
+          if (i < n_items) {
+            const int64_t e = static_cast<int64_t>(tok0 + i / cpt) * a.D + (i % cpt) * 8;
+            kk[u] = ld16(sk + e);
+            vv[u] = ld16(sv + e);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kPackPer; ++u) {
+          const int i = base + threadIdx.x + u * kPackThreads;
+          if (i >= n_items) continue;
+          const int tok = tok0 + i / cpt, ch = i % cpt;
+          const int64_t e = static_cast<int64_t>(tok) * a.D + ch * 8;
+          uint4 k4 = kk[u];
+          if (rope) {
+            const int64_t *pp = sp + static_cast<int64_t>(tok) * 3;
+            const int64_t t = tr >= 0 ? tr : pp[0];
+            k4 = rope_chunk(k4, ch, t, pp[1], pp[2], a.rope);
+          }
+          st16_nt(ok + e, k4);
+          st16_nt(ov + e, vv[u]);
         }
       }
-#pragma unroll
-      for (int u = 0; u < kPackPer; ++u) {
-        const int i = base + threadIdx.x + u * kPackThreads;
-        if (i >= n_items) continue;
-        const int tok = tok0 + i / cpt, ch = i % cpt;
-        const int64_t e = static_cast<int64_t>(tok) * a.D + ch * 8;
-        uint4 k4 = kk[u];
-        if (rope) {
-          const int64_t *pp = sp + static_cast<int64_t>(tok) * 3;
-          const int64_t t = tr >= 0 ? tr : pp[0];
-          k4 = rope_chunk(k4, ch, t, pp[1], pp[2], a.rope);
+      if (a.pos_out && sp) {
+        int64_t *op = a.pos_out + dst * 3;
+        for (int i = threadIdx.x; i < ntok * 3; i += blockDim.x) {
+          const int64_t e = static_cast<int64_t>(tok0) * 3 + i;
+          op[e] = sp[e];
         }
-        st16_nt(ok + e, k4);
-        st16_nt(ov + e, vv[u]);
       }
-    }
-    if (a.pos_out && sp) {
-      int64_t *op = a.pos_out + dst * 3;
-      for (int i = threadIdx.x; i < ntok * 3; i += blockDim.x) {
-        const int64_t e = static_cast<int64_t>(tok0) * 3 + i;
-        op[e] = sp[e];
-      }
-    }
+    }  // tiles of a long segment
   }
 }
 

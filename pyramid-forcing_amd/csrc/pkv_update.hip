@@ -864,7 +864,7 @@ static PoolPtrs pool_ptrs(const pkv_geometry *g, const pkv_pools *p) {
   return pp;
 }
 
-static int check_geometry(const pkv_geometry *g) {
+int check_geometry(const pkv_geometry *g) {
   if (!g) return fail(PKV_ERR_INVALID, "geometry is NULL");
   if (g->num_layers <= 0 || g->num_heads <= 0 || g->head_dim <= 0 || g->frame_seqlen <= 0)
     return fail(PKV_ERR_INVALID, "geometry: num_layers/num_heads/head_dim/frame_seqlen must be > 0");

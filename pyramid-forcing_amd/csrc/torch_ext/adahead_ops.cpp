@@ -651,6 +651,191 @@ static void cache_update(Mgr mgr, Tensor states_layer, Tensor sink_caps_layer, T
 
 static std::vector<Tensor> update_descriptors(Mgr mgr, int64_t frames) { return mgr->update_descriptors(frames); }
 
+// ---------------------------------------------------------------------------
+// data-movement ops of the _ops.py surface (scatter_copy_bind.cpp:451-683)
+// and the legacy planner (pyramidkv_plan.cc:46-133)
+// ---------------------------------------------------------------------------
+static void check_dev_i64(const Tensor &t, const char *name, int64_t n) {
+  TORCH_CHECK(t.is_cuda(), name, " must be on CUDA");
+  TORCH_CHECK(t.dtype() == at::kLong, name, " must be int64");
+  TORCH_CHECK(t.dim() == 1, name, " must be 1D");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK(t.size(0) >= n, name, " is too small");
+}
+
+static void scatter_copy(Tensor src_ptrs, Tensor lengths, Tensor offsets, Tensor dst, int64_t col_dim) {
+  TORCH_CHECK(src_ptrs.is_cuda(), "src_ptrs must be on CUDA");
+  TORCH_CHECK(dst.is_cuda(), "dst must be on CUDA");
+  TORCH_CHECK(src_ptrs.dtype() == at::kLong, "src_ptrs must be int64");
+  const int64_t n = src_ptrs.size(0);
+  if (n == 0) return;
+  check_dev_i64(src_ptrs, "src_ptrs", n);
+  check_dev_i64(lengths, "lengths", n);
+  check_dev_i64(offsets, "offsets", n);
+  TORCH_CHECK(dst.is_contiguous(), "dst must be contiguous");
+  TORCH_CHECK(col_dim > 0, "col_dim must be > 0");
+  const int64_t row_bytes = col_dim * static_cast<int64_t>(dst.element_size());
+  const int64_t dst_rows = dst.numel() / col_dim;
+  pkv_check(pkv_scatter_copy(src_ptrs.data_ptr<int64_t>(), lengths.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
+                             static_cast<int32_t>(n), dst.data_ptr(), dst_rows, row_bytes, stream_for(dst)),
+            "scatter_copy");
+}
+
+static void apply_pos_override(Tensor pos, Tensor starts, Tensor ends, Tensor vals) {
+  TORCH_CHECK(pos.is_cuda(), "pos must be on CUDA");
+  TORCH_CHECK(pos.size(1) == 3, "pos must have 3 columns");
+  const int64_t m = starts.size(0);
+  if (m == 0) return;
+  TORCH_CHECK(pos.dtype() == at::kLong && pos.is_contiguous(), "pos must be contiguous int64 [N, 3]");
+  check_dev_i64(starts, "starts", m);
+  check_dev_i64(ends, "ends", m);
+  check_dev_i64(vals, "vals", m);
+  pkv_check(pkv_pos_override(pos.data_ptr<int64_t>(), pos.size(0), starts.data_ptr<int64_t>(),
+                             ends.data_ptr<int64_t>(), vals.data_ptr<int64_t>(), static_cast<int32_t>(m),
+                             stream_for(pos)),
+            "apply_pos_override");
+}
+
+static int32_t mapping_mode_code(const std::string &mode) {
+  if (mode == "relative_clamp") return 1;
+  if (mode == "relative_softcap") return 2;
+  return 0;  // "none" and unknown modes (scatter_copy_bind.cpp:481-486)
+}
+
+// device pointers of the tensors -> int64 device tensor (synchronous copy
+// from a host tensor, so the host buffer outlives the transfer)
+static void fill_ptrs(const std::vector<Tensor> &ts, Tensor dst, const char *name) {
+  std::vector<int64_t> host;
+  host.reserve(ts.size());
+  c10::optional<c10::Device> dev;
+  for (size_t i = 0; i < ts.size(); ++i) {
+    TORCH_CHECK(ts[i].is_cuda(), name, "[", i, "] must be on CUDA");
+    TORCH_CHECK(ts[i].is_contiguous(), name, "[", i, "] must be contiguous");
+    if (!dev) dev = ts[i].device();
+    TORCH_CHECK(ts[i].device() == *dev, name, "[", i, "] is on a different CUDA device");
+    host.push_back(reinterpret_cast<int64_t>(ts[i].data_ptr()));
+  }
+  if (host.empty()) return;
+  auto cpu = at::from_blob(host.data(), {static_cast<int64_t>(host.size())}, at::TensorOptions().dtype(at::kLong));
+  dst.narrow(0, 0, static_cast<int64_t>(host.size())).copy_(cpu, /*non_blocking=*/false);
+}
+
+static void refresh_readout_layout(std::vector<Tensor> src_k, std::vector<Tensor> src_v, std::vector<Tensor> src_pos,
+                                   Tensor src_ptrs_k, Tensor src_ptrs_v, Tensor src_ptrs_pos, Tensor offsets,
+                                   Tensor lengths, Tensor flags, Tensor dynamic_rope_t, Tensor dst_k_raw,
+                                   Tensor dst_v, Tensor dst_rope_pos, Tensor dst_frame_ids, int64_t head_dim,
+                                   int64_t current_t, std::string history_time_mapping_mode,
+                                   int64_t history_relative_t_max, double history_time_soft_factor) {
+  const int64_t n = static_cast<int64_t>(src_k.size());
+  TORCH_CHECK(src_v.size() == src_k.size(), "src_v length must match src_k");
+  TORCH_CHECK(src_pos.size() == src_k.size(), "src_pos length must match src_k");
+  if (n == 0) return;
+  TORCH_CHECK(dst_k_raw.is_cuda() && dst_v.is_cuda() && dst_rope_pos.is_cuda() && dst_frame_ids.is_cuda(),
+              "refresh_readout_layout: outputs must be on CUDA");
+  TORCH_CHECK(dst_rope_pos.dtype() == at::kLong, "dst_rope_pos must be int64");
+  TORCH_CHECK(dst_frame_ids.dtype() == at::kLong, "dst_frame_ids must be int64");
+  TORCH_CHECK(dst_k_raw.is_contiguous() && dst_v.is_contiguous() && dst_rope_pos.is_contiguous() &&
+                  dst_frame_ids.is_contiguous(),
+              "refresh_readout_layout: outputs must be contiguous");
+  TORCH_CHECK(dst_k_raw.dtype() == dst_v.dtype(), "dst_k_raw/dst_v dtype mismatch");
+  TORCH_CHECK(dst_k_raw.size(1) == head_dim, "dst_k_raw head_dim mismatch");
+  TORCH_CHECK(dst_v.size(1) == head_dim, "dst_v head_dim mismatch");
+  TORCH_CHECK(dst_rope_pos.size(1) == 3, "dst_rope_pos must have 3 columns");
+  TORCH_CHECK(dst_v.size(0) == dst_k_raw.size(0) && dst_rope_pos.size(0) == dst_k_raw.size(0) &&
+                  dst_frame_ids.size(0) >= dst_k_raw.size(0),
+              "refresh_readout_layout: output row counts differ");
+  for (const Tensor *t : {&src_ptrs_k, &src_ptrs_v, &src_ptrs_pos, &offsets, &lengths, &flags, &dynamic_rope_t}) {
+    check_dev_i64(*t, "refresh_readout_layout descriptor", n);
+    TORCH_CHECK(t->device() == dst_k_raw.device(), "descriptor device mismatch");
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    TORCH_CHECK(src_k[i].dtype() == dst_k_raw.dtype(), "src_k dtype mismatch");
+    TORCH_CHECK(src_v[i].dtype() == dst_v.dtype(), "src_v dtype mismatch");
+    TORCH_CHECK(src_pos[i].dtype() == at::kLong, "src_pos must be int64");
+    TORCH_CHECK(src_k[i].size(1) == head_dim, "src_k head_dim mismatch");
+    TORCH_CHECK(src_v[i].size(1) == head_dim, "src_v head_dim mismatch");
+    TORCH_CHECK(src_pos[i].size(1) == 3, "src_pos must have 3 columns");
+    TORCH_CHECK(src_k[i].device() == dst_k_raw.device(), "src_k device mismatch");
+  }
+  fill_ptrs(src_k, src_ptrs_k, "src_k");
+  fill_ptrs(src_v, src_ptrs_v, "src_v");
+  fill_ptrs(src_pos, src_ptrs_pos, "src_pos");
+  pkv_refresh_args a;
+  a.src_ptrs_k = src_ptrs_k.data_ptr<int64_t>();
+  a.src_ptrs_v = src_ptrs_v.data_ptr<int64_t>();
+  a.src_ptrs_pos = src_ptrs_pos.data_ptr<int64_t>();
+  a.offsets = offsets.data_ptr<int64_t>();
+  a.lengths = lengths.data_ptr<int64_t>();
+  a.flags = flags.data_ptr<int64_t>();
+  a.dynamic_rope_t = dynamic_rope_t.data_ptr<int64_t>();
+  a.dst_k = dst_k_raw.data_ptr();
+  a.dst_v = dst_v.data_ptr();
+  a.dst_pos = dst_rope_pos.data_ptr<int64_t>();
+  a.dst_frame_ids = dst_frame_ids.data_ptr<int64_t>();
+  a.dst_rows = dst_k_raw.size(0);
+  a.row_bytes = head_dim * static_cast<int64_t>(dst_k_raw.element_size());
+  a.current_t = current_t;
+  a.history_relative_t_max = history_relative_t_max;
+  a.n_segments = static_cast<int32_t>(n);
+  a.history_mode_code = mapping_mode_code(history_time_mapping_mode);
+  a.history_soft_factor = static_cast<float>(history_time_soft_factor);
+  pkv_check(pkv_refresh_readout(&a, stream_for(dst_k_raw)), "refresh_readout_layout");
+}
+
+static void anchor_store_write_frames(Tensor k_seq, Tensor v_seq, Tensor pos_seq, Tensor frame_desc, Tensor store_k,
+                                      Tensor store_v, Tensor store_pos) {
+  for (const Tensor *t : {&k_seq, &v_seq, &pos_seq, &frame_desc, &store_k, &store_v, &store_pos}) {
+    TORCH_CHECK(t->is_cuda(), "anchor_store_write_frames: tensors must be on CUDA");
+    TORCH_CHECK(t->is_contiguous(), "anchor_store_write_frames: tensors must be contiguous");
+  }
+  TORCH_CHECK(k_seq.dtype() == store_k.dtype(), "k_seq/store_k dtype mismatch");
+  TORCH_CHECK(v_seq.dtype() == store_v.dtype(), "v_seq/store_v dtype mismatch");
+  TORCH_CHECK(pos_seq.dtype() == at::kLong, "pos_seq must be int64");
+  TORCH_CHECK(store_pos.dtype() == at::kLong, "store_pos must be int64");
+  TORCH_CHECK(frame_desc.dtype() == at::kLong, "frame_desc must be int64");
+  TORCH_CHECK(k_seq.dim() == 2, "k_seq must be [tokens, head_dim]");
+  TORCH_CHECK(v_seq.dim() == 2 && v_seq.sizes() == k_seq.sizes(), "v_seq must be [tokens, head_dim]");
+  TORCH_CHECK(pos_seq.dim() == 2 && pos_seq.size(1) == 3 && pos_seq.size(0) == k_seq.size(0),
+              "pos_seq must be [tokens, 3]");
+  TORCH_CHECK(frame_desc.dim() == 2 && frame_desc.size(1) == 2, "frame_desc must be [N, 2]");
+  TORCH_CHECK(store_k.dim() == 3, "store_k must be [capacity, frame_seqlen, head_dim]");
+  TORCH_CHECK(store_v.dim() == 3 && store_v.sizes() == store_k.sizes(),
+              "store_v must be [capacity, frame_seqlen, head_dim]");
+  TORCH_CHECK(store_pos.dim() == 3 && store_pos.size(2) == 3 && store_pos.size(0) == store_k.size(0) &&
+                  store_pos.size(1) == store_k.size(1),
+              "store_pos must be [capacity, frame_seqlen, 3]");
+  TORCH_CHECK(k_seq.size(1) == store_k.size(2), "head_dim mismatch");
+  const int64_t n = frame_desc.size(0);
+  if (n == 0) return;
+  const int64_t fs = store_k.size(1);
+  const int64_t row_bytes = store_k.size(2) * static_cast<int64_t>(store_k.element_size());
+  pkv_check(pkv_anchor_store_write_frames(k_seq.data_ptr(), v_seq.data_ptr(), pos_seq.data_ptr<int64_t>(),
+                                          k_seq.size(0) / fs, frame_desc.data_ptr<int64_t>(), static_cast<int32_t>(n),
+                                          store_k.data_ptr(), store_v.data_ptr(), store_pos.data_ptr<int64_t>(),
+                                          store_k.size(0), fs, row_bytes, stream_for(store_k)),
+            "anchor_store_write_frames");
+}
+
+using Plan5 = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>;
+
+// Legacy plan over all layers and heads (pyramidkv_plan.cc:46-133): fresh
+// device tensors, built on the device from valid_count (no host round trip).
+static Plan5 pyramidkv_plan(Mgr mgr, int64_t current_t, int64_t pass_kind) {
+  TORCH_CHECK(mgr.get() != nullptr, "pyramidkv_plan: manager is null");
+  (void)current_t;
+  (void)pass_kind;
+  const int64_t N = mgr->num_layers() * mgr->num_heads();
+  auto o32 = at::TensorOptions().dtype(at::kInt).device(mgr->valid_count().device());
+  Tensor cu = at::empty({N + 1}, o32), sk = at::empty({3 * N}, o32), sg = at::empty({3 * N}, o32),
+         sl = at::empty({3 * N}, o32), dst = at::empty({3 * N}, o32);
+  const pkv_geometry g = mgr->geometry();
+  pkv_check(pkv_plan_legacy(&g, mgr->valid_count().data_ptr<int64_t>(), cu.data_ptr<int32_t>(),
+                            sk.data_ptr<int32_t>(), sg.data_ptr<int32_t>(), sl.data_ptr<int32_t>(),
+                            dst.data_ptr<int32_t>(), stream_for(cu)),
+            "pyramidkv_plan");
+  return {cu, sk, sg, sl, dst};
+}
+
 // MegaCache.attend's K/V side (pkv_plan_pack): plan for the chunks of
 // current_t_list with layer offsets folded in, then pack (+RoPE when the
 // three tables are non-empty) into the manager's flat outputs.  Returns the
@@ -724,6 +909,12 @@ static Tensor attn(Tensor q, Tensor, Tensor, Tensor, Tensor, int64_t, double, bo
 static Tensor rope(Tensor k, Tensor, Tensor, Tensor, Tensor) { return at::empty_like(k); }
 static void cache_update(Mgr, Tensor, Tensor, Tensor, Tensor, Tensor, int64_t, int64_t, int64_t, int64_t, int64_t,
                          bool) {}
+static void scatter_copy(Tensor, Tensor, Tensor, Tensor, int64_t) {}
+static void pos_override(Tensor, Tensor, Tensor, Tensor) {}
+static void write_frames(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor) {}
+static void refresh(std::vector<Tensor>, std::vector<Tensor>, std::vector<Tensor>, Tensor, Tensor, Tensor, Tensor,
+                    Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, int64_t, int64_t, std::string, int64_t,
+                    double) {}
 }  // namespace adahead_meta
 
 TORCH_LIBRARY(adahead, m) {
@@ -817,6 +1008,17 @@ TORCH_LIBRARY(adahead, m) {
         "Tensor sink_caps_layer, Tensor(b!) committed_vc_layer, Tensor new_k, Tensor new_v, int layer, int t0, "
         "int pass_kind, int shift_pending, int spatial_width, bool has_merge_head) -> ()");
   m.def("update_descriptors(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, int frames) -> Tensor[]");
+  m.def("scatter_copy(Tensor src_ptrs, Tensor lengths, Tensor offsets, Tensor(a!) dst, int col_dim) -> ()");
+  m.def("apply_pos_override(Tensor(a!) pos, Tensor starts, Tensor ends, Tensor vals) -> ()");
+  m.def("anchor_store_write_frames(Tensor k_seq, Tensor v_seq, Tensor pos_seq, Tensor frame_desc, "
+        "Tensor(a!) store_k, Tensor(b!) store_v, Tensor(c!) store_pos) -> ()");
+  m.def("refresh_readout_layout(Tensor[] src_k, Tensor[] src_v, Tensor[] src_pos, Tensor(a!) src_ptrs_k, "
+        "Tensor(b!) src_ptrs_v, Tensor(c!) src_ptrs_pos, Tensor offsets, Tensor lengths, Tensor flags, "
+        "Tensor dynamic_rope_t, Tensor(d!) dst_k_raw, Tensor(e!) dst_v, Tensor(f!) dst_rope_pos, "
+        "Tensor(g!) dst_frame_ids, int head_dim, int current_t, str history_time_mapping_mode, "
+        "int history_relative_t_max, float history_time_soft_factor) -> ()");
+  m.def("pyramidkv_plan(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, int current_t, int pass_kind) "
+        "-> (Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("mega_attend_kv(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, Tensor states_layer, "
         "int layer_idx, Tensor current_t_list, int sink_mode_code, int sink_clamp_min, int sink_clamp_max, "
         "int decoupled_sink_lag, Tensor freqs_ft_flat, Tensor freqs_fy_flat, Tensor freqs_fx_flat) -> Tensor");
@@ -831,6 +1033,10 @@ TORCH_LIBRARY_IMPL(adahead, CUDA, m) {
   m.impl("ragged_attention", adahead::ragged_attention);
   m.impl("rope_apply", adahead::rope_apply);
   m.impl("cache_update", adahead::cache_update);
+  m.impl("scatter_copy", adahead::scatter_copy);
+  m.impl("apply_pos_override", adahead::apply_pos_override);
+  m.impl("anchor_store_write_frames", adahead::anchor_store_write_frames);
+  m.impl("refresh_readout_layout", adahead::refresh_readout_layout);
 }
 
 // Ops whose only tensor arguments may live on the host, or that take none,
@@ -841,6 +1047,7 @@ TORCH_LIBRARY_IMPL(adahead, CompositeExplicitAutograd, m) {
   m.impl("mega_plan_multi", adahead::mega_plan_multi);
   m.impl("update_descriptors", adahead::update_descriptors);
   m.impl("mega_attend_kv", adahead::mega_attend_kv);
+  m.impl("pyramidkv_plan", adahead::pyramidkv_plan);
 }
 
 TORCH_LIBRARY_IMPL(adahead, Meta, m) {
@@ -854,4 +1061,8 @@ TORCH_LIBRARY_IMPL(adahead, Meta, m) {
   m.impl("ragged_attention", adahead_meta::attn);
   m.impl("rope_apply", adahead_meta::rope);
   m.impl("cache_update", adahead_meta::cache_update);
+  m.impl("scatter_copy", adahead_meta::scatter_copy);
+  m.impl("apply_pos_override", adahead_meta::pos_override);
+  m.impl("anchor_store_write_frames", adahead_meta::write_frames);
+  m.impl("refresh_readout_layout", adahead_meta::refresh);
 }

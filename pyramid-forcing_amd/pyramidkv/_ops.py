@@ -66,3 +66,29 @@ def ragged_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_
         softmax_scale = q.shape[-1] ** -0.5
     return ops().ragged_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), float(softmax_scale),
                                   bool(kv_per_head), bool(causal))
+
+
+def scatter_copy(src_ptrs, lengths, offsets, dst, col_dim: int) -> None:
+    """Gather rows from the device addresses in ``src_ptrs`` into ``dst``."""
+    ops().scatter_copy(src_ptrs, lengths, offsets, dst, int(col_dim))
+
+
+def apply_pos_override(pos, starts, ends, vals) -> None:
+    """pos[i, 0] = vals[r] for starts[r] <= i < ends[r]."""
+    ops().apply_pos_override(pos, starts, ends, vals)
+
+
+def anchor_store_write_frames(k_seq, v_seq, pos_seq, frame_desc, store_k, store_v, store_pos) -> None:
+    """Copy frames (frame_desc rows: source frame, store slot) into store slots."""
+    ops().anchor_store_write_frames(k_seq, v_seq, pos_seq, frame_desc, store_k, store_v, store_pos)
+
+
+def refresh_readout_layout(src_k, src_v, src_pos, src_ptrs_k, src_ptrs_v, src_ptrs_pos, offsets, lengths, flags,
+                           dynamic_rope_t, dst_k_raw, dst_v, dst_rope_pos, dst_frame_ids, head_dim: int,
+                           current_t: int, history_time_mapping_mode: str, history_relative_t_max: int,
+                           history_time_soft_factor: float) -> None:
+    """K/V gather with the history time map and frame ids (see the op)."""
+    ops().refresh_readout_layout(src_k, src_v, src_pos, src_ptrs_k, src_ptrs_v, src_ptrs_pos, offsets, lengths,
+                                 flags, dynamic_rope_t, dst_k_raw, dst_v, dst_rope_pos, dst_frame_ids,
+                                 int(head_dim), int(current_t), str(history_time_mapping_mode),
+                                 int(history_relative_t_max), float(history_time_soft_factor))
