@@ -2,14 +2,16 @@
 // accumulation, MFMA v_mfma_f32_32x32x16_bf16.  Replaces the reference's
 // flash_attn_varlen_func call (pyramidkv/_mega_cache.py:540-559).
 //
-// Work decomposition.  A workgroup of 4 waves owns 128 query rows (32 per
+// Work decomposition.  A workgroup of 8 waves owns 256 query rows (32 per
 // wave) of one (query sequence, head) pair and streams that pair's keys in
-// tiles of 64 through double-buffered LDS, one barrier per tile.  Two
-// workgroups share a CU (each wave stays within 256 registers), so every SIMD
-// runs two waves whose MFMA and softmax phases interleave.  All 256 threads
-// stage both K and V: 16-byte buffer loads bounded at the sequence's last row
-// (rows past the end read as zero), prefetched one tile ahead, stored
-// row-major into LDS with 16-byte stores.
+// tiles of 64 through double-buffered LDS, one barrier per tile; one
+// workgroup per CU, so every SIMD runs two waves (each within 256 registers)
+// whose MFMA and softmax phases interleave.  All 512 threads stage both K and
+// V: 16-byte buffer loads bounded at the sequence's last row (rows past the
+// end read as zero), issued two tiles ahead, stored row-major into LDS with
+// 16-byte stores.  Each staged tile serves 256 query rows, which halves the
+// load and LDS-store traffic per flop of a 128-row workgroup.  The order of
+// the work items balances the XCDs (balanced_item).
 //
 // Operand arrangement.  The wave computes S^T = K * Q^T (A = K rows read
 // from LDS, B = Q^T kept in registers), so the 32x32 MFMA result gives every
@@ -40,10 +42,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBK = 64;  // keys per LDS tile
 constexpr float kLazy = 8.0f;
+constexpr int kSchedMax = 1024;  // sequences the XCD-balanced schedule handles
 
 struct AttnParams {
   const uint16_t *q, *k, *v;
@@ -55,12 +58,93 @@ struct AttnParams {
 };
 
 // Consecutive workgroup ids are dispatched round-robin over the 8 XCDs;
-// renumber them so that the query tiles of one sequence (which share its
-// keys) run on the same XCD and share its L2.
+// renumber them so that XCD x runs the contiguous index range
+// [start_x, start_x + count_x) of the work list, in increasing order.
 __device__ inline int xcd_remap(int i, int n) {
   const int xcd = i % 8, k = i / 8;
   const int base = n / 8, rem = n % 8;
   return xcd < rem ? xcd * (base + 1) + k : rem * (base + 1) + (xcd - rem) * base + k;
+}
+
+// Work list of (sequence, query tile) items, computed by every workgroup in
+// its prologue (a few microseconds, no workspace, no extra launch).  A
+// sequence's cost is its query tiles times its key tiles.  Sequences are
+// ranked by cost (largest first, ties by index) and dealt to 8 bins in snake
+// order (ranks 0..7 to bins 0..7, ranks 8..15 to bins 7..0, ...), each bin
+// keeping the ranked order; the list is the bins' items concatenated, a
+// sequence's query tiles consecutive.  With xcd_remap each XCD then runs one
+// bin: balanced work per XCD (its own L2 holds the keys its query tiles
+// share) and the longest sequences first.  Every step is parallel over the
+// sequences.  Returns false when this workgroup has no item.  scratch:
+// 4 * kSchedMax ints of LDS, 16-byte aligned; every thread of the workgroup
+// must call it.
+__device__ inline int snake_bin(int p) { return ((p >> 3) & 1) ? 7 - (p & 7) : (p & 7); }
+
+__device__ bool balanced_item(const int32_t *cu_q, const int32_t *cu_k, int Hq, int n_seq, int kv_per_head, int bq,
+                              int c, int *scratch, int &seq_out, int &qt_out) {
+  int *cost = scratch, *order = scratch + kSchedMax, *qts = scratch + 2 * kSchedMax, *off = scratch + 3 * kSchedMax;
+  __shared__ int res[2];
+  __shared__ int btot[8];
+  const int n4 = (n_seq + 3) & ~3;
+  for (int s = threadIdx.x; s < n4; s += blockDim.x) {
+    int nq = 0, cs = -1;  // padding entries rank after every sequence
+    if (s < n_seq) {
+      const int b = s / Hq;
+      nq = (cu_q[b + 1] - cu_q[b] + bq - 1) / bq;
+      const int kv = kv_per_head ? s : b;
+      cs = nq * ((cu_k[kv + 1] - cu_k[kv] + 63) / 64 + 1);  // +1: fixed cost per query tile
+    }
+    qts[s] = nq;
+    cost[s] = cs;
+  }
+  if (threadIdx.x < 8) btot[threadIdx.x] = 0;
+  if (threadIdx.x == 0) {
+    res[0] = -1;
+    res[1] = 0;
+  }
+  __syncthreads();
+  // rank = number of sequences before s in (cost desc, index asc) order;
+  // the costs are read four at a time (the same address across the wave)
+  for (int s = threadIdx.x; s < n_seq; s += blockDim.x) {
+    const int cs = cost[s];
+    int r = 0;
+    const int4 *c4 = reinterpret_cast<const int4 *>(cost);
+#pragma unroll 4
+    for (int t4 = 0; t4 < n4 / 4; ++t4) {
+      const int4 v = c4[t4];
+      const int t = 4 * t4;
+      r += (v.x > cs) || (v.x == cs && t < s);
+      r += (v.y > cs) || (v.y == cs && t + 1 < s);
+      r += (v.z > cs) || (v.z == cs && t + 2 < s);
+      r += (v.w > cs) || (v.w == cs && t + 3 < s);
+    }
+    order[r] = s;
+  }
+  __syncthreads();
+  // rank p: its bin, its item offset within the bin, the bin totals
+  for (int p = threadIdx.x; p < n_seq; p += blockDim.x) {
+    const int x = snake_bin(p), k = p >> 3;
+    int o = 0;
+#pragma unroll 4
+    for (int kk = 0; kk < k; ++kk) o += qts[order[8 * kk + ((kk & 1) ? 7 - x : x)]];
+    off[p] = o;
+    atomicAdd(&btot[x], qts[order[p]]);
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < n_seq; p += blockDim.x) {
+    const int x = snake_bin(p);
+    int base = off[p];
+    for (int xx = 0; xx < x; ++xx) base += btot[xx];
+    const int sq = order[p];
+    if (c >= base && c < base + qts[sq]) {
+      res[0] = sq;
+      res[1] = c - base;
+    }
+  }
+  __syncthreads();
+  seq_out = res[0];
+  qt_out = res[1];
+  return seq_out >= 0;
 }
 
 __device__ inline uint4 ldg16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -94,19 +178,36 @@ __device__ inline float half_sum(float x) {
 }
 
 template <int D>
-__global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
+__global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
   constexpr int BQ = 32 * kWaves;
   constexpr int DS = D / 16;  // k-steps of the QK^T product
   constexpr int DB = D / 32;  // 32-row blocks of O^T
-  constexpr int RS = D + 8;   // LDS row stride (elements) of K and V; +16 B spreads the banks
+  // LDS row strides (elements).  K rows are read 16 bytes per lane, 32
+  // rows at a time: +16 B per row puts 16 consecutive rows on distinct
+  // banks.  V rows are read by the transpose read, 4 rows x 64 B per 32
+  // lanes: +64 B per row puts those 4 rows on distinct banks.
+  constexpr int RS = D + 8;
+  constexpr int RSV = D + 32;
   constexpr int KCH = D / 8;  // 16-byte chunks per row
   constexpr int LD = kBK * KCH / kThreads;  // 16-byte loads per thread per tile, each of K and V
   static_assert(LD * kThreads == kBK * KCH && LD <= 4, "tile split");
+  static_assert(2 * kBK * RS * 2 >= 4 * kSchedMax * 4, "schedule scratch fits in the K tiles");
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBK * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBK * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBK * RSV];
 
-  const int wg = xcd_remap(blockIdx.x, p.n_wg);
-  const int seq = wg / p.q_tiles, qt = wg % p.q_tiles;
+  int seq, qt;
+  const int n_seq = p.n_wg / p.q_tiles;
+  if (n_seq <= kSchedMax) {
+    // the schedule's scratch is the K tiles, not yet in use
+    // (its last barrier orders every scratch read before the first K store)
+    if (!balanced_item(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, BQ, xcd_remap(blockIdx.x, p.n_wg),
+                       reinterpret_cast<int *>(&Ks[0][0]), seq, qt))
+      return;
+  } else {
+    const int wg = xcd_remap(blockIdx.x, p.n_wg);
+    seq = wg / p.q_tiles;
+    qt = wg % p.q_tiles;
+  }
   const int b = seq / p.Hq, h = seq % p.Hq;
   const int q_begin = p.cu_q[b];
   const int Lq = p.cu_q[b + 1] - q_begin;
@@ -151,14 +252,20 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
   // two register sets: tile t is loaded into set t%2 two iterations before
   // it is stored, so each load has two tile-times to arrive
   uint4 sk[2][LD], sv[2][LD];
+  // A tile at or past the sequence's end gets a resource with no records:
+  // its loads return zero without touching memory, so the loop can load
+  // every tile unconditionally (no branch around a load keeps the compiler's
+  // outstanding-load accounting exact, and each wait covers only the tile
+  // that is about to be stored).
   auto load_tile = [&](int kt, uint4 (&k4)[LD], uint4 (&v4)[LD]) {
     const int64_t first = static_cast<int64_t>(kt) * kBK;
     const int64_t left = (static_cast<int64_t>(Lk) - first) * row_elems * 2;
-    const int nrec = static_cast<int>(left < 0x7fffffff ? left : 0x7fffffff);
+    const int nrec = static_cast<int>(left <= 0 ? 0 : (left < 0x7fffffff ? left : 0x7fffffff));
+    const int64_t base = left <= 0 ? 0 : first * row_elems;
     const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kp + first * row_elems), 0, nrec, kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kp + base), 0, nrec, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vp + first * row_elems), 0, nrec, kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vp + base), 0, nrec, kRsrcWord3);
 #pragma unroll
     for (int r = 0; r < LD; ++r) {
       const int idx = tid + r * kThreads;
@@ -171,9 +278,8 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
 #pragma unroll
     for (int r = 0; r < LD; ++r) {
       const int idx = tid + r * kThreads;
-      const int e = (idx / KCH) * RS + (idx % KCH) * 8;
-      *reinterpret_cast<uint4 *>(&Ks[buf][e]) = k4[r];
-      *reinterpret_cast<uint4 *>(&Vs[buf][e]) = v4[r];
+      *reinterpret_cast<uint4 *>(&Ks[buf][(idx / KCH) * RS + (idx % KCH) * 8]) = k4[r];
+      *reinterpret_cast<uint4 *>(&Vs[buf][(idx / KCH) * RSV + (idx % KCH) * 8]) = v4[r];
     }
   };
 
@@ -205,9 +311,15 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
         if (key + 32 >= Lk) s1[i] = -INFINITY;
       }
     }
-    float mx = fmaxf(s0[0], s1[0]);
+    // maximum and sum as 4-way trees, not one serial chain each
+    float mq[4];
 #pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, fmaxf(s0[i], s1[i]));
+    for (int r = 0; r < 4; ++r) {
+      mq[r] = fmaxf(s0[r], s1[r]);
+#pragma unroll
+      for (int i = r + 4; i < 16; i += 4) mq[r] = fmaxf(mq[r], fmaxf(s0[i], s1[i]));
+    }
+    float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
     mx = half_max(mx) * c;
     const bool move = mx > m + kLazy || m == -INFINITY;
     float alpha = 1.0f;
@@ -215,7 +327,7 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
       alpha = __builtin_amdgcn_exp2f(m - mx);
       m = mx;
     }
-    float ps = 0.0f;
+    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     bf16x8 pb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -223,10 +335,10 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
       for (int j = 0; j < 8; ++j) {
         const float sv_ = ks < 2 ? s0[8 * ks + j] : s1[8 * (ks - 2) + j];
         const float e = __builtin_amdgcn_exp2f(fmaf(sv_, c, -m));
-        ps += e;
+        ps[j & 3] += e;
         pb[ks][j] = static_cast<__bf16>(e);
       }
-    l = l * alpha + ps;
+    l = l * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
     if (__any(move)) {
       // in place (tied operands), so the accumulators keep their registers
 #pragma unroll
@@ -238,40 +350,50 @@ __global__ void __launch_bounds__(kThreads, 2) attn_fwd_kernel(AttnParams p) {
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const uint16_t *vptr = &Vs[buf][(16 * ks + v_row) * RS + db * 32 + v_col];
-        const i16x4 lo = lds_tr16(vptr), hi = lds_tr16(vptr + 8 * RS);
+        const uint16_t *vptr = &Vs[buf][(16 * ks + v_row) * RSV + db * 32 + v_col];
+        const i16x4 lo = lds_tr16(vptr), hi = lds_tr16(vptr + 8 * RSV);
         const i16x4 a8[2] = {lo, hi};
         const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
       }
   };
 
-  const int n_tiles = (Lk + kBK - 1) / kBK;
-  if (n_tiles > 0) {
+  // The loop runs whole pairs of tiles: with an odd tile count the last
+  // step sees a tile wholly past the end, whose keys are all masked and
+  // which adds nothing to O or l.
+  const int n_pairs = (Lk + 2 * kBK - 1) / (2 * kBK);
+  if (n_pairs > 0) {
+    // the issue order tile 1 then tile 2 is kept (scheduling barriers), so
+    // that on entering the loop the loads of tile 1 are older than those of
+    // tile 2, as they are on every later iteration, and the first store of
+    // the loop waits for tile 1's loads only
     load_tile(0, sk[0], sv[0]);
     store_tile(0, sk[0], sv[0]);
-  }
-  if (n_tiles > 1) load_tile(1, sk[1], sv[1]);
-  if (n_tiles > 2) load_tile(2, sk[0], sv[0]);
-  // iteration kt: tile kt is in LDS buffer kt%2; tile kt+1 (register set
-  // (kt+1)%2) is stored into the other buffer, then tile kt+3 is loaded into
-  // the set just freed
-  auto step = [&](int kt, uint4 (&k4)[LD], uint4 (&v4)[LD]) {
-    const int buf = kt & 1;
-    __syncthreads();  // tile kt visible; every wave is done with buffer buf^1
-    if (kt + 1 < n_tiles) store_tile(buf ^ 1, k4, v4);
-    if (kt + 3 < n_tiles) load_tile(kt + 3, k4, v4);
-    // the QK^T MFMA cluster runs at raised wave priority, so a wave that
-    // reaches it issues ahead of its SIMD partner's softmax VALU work
-    __builtin_amdgcn_s_setprio(2);
-    const f32x16 s0 = qk(buf, 0);
-    const f32x16 s1 = qk(buf, 1);
-    __builtin_amdgcn_s_setprio(0);
-    consume(s0, s1, buf, kt * kBK);
-  };
-  for (int kt = 0; kt < n_tiles; kt += 2) {
-    step(kt, sk[1], sv[1]);
-    if (kt + 1 < n_tiles) step(kt + 1, sk[0], sv[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(1, sk[1], sv[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(2, sk[0], sv[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    // iteration kt: tile kt is in LDS buffer kt%2; tile kt+1 (register set
+    // (kt+1)%2) is stored into the other buffer, then tile kt+3 is loaded
+    // into the set just freed
+    auto step = [&](int kt, uint4 (&k4)[LD], uint4 (&v4)[LD]) {
+      const int buf = kt & 1;
+      __syncthreads();  // tile kt visible; every wave is done with buffer buf^1
+      store_tile(buf ^ 1, k4, v4);
+      load_tile(kt + 3, k4, v4);
+      // the QK^T MFMA cluster runs at raised wave priority, so a wave that
+      // reaches it issues ahead of its SIMD partner's softmax VALU work
+      __builtin_amdgcn_s_setprio(2);
+      const f32x16 s0 = qk(buf, 0);
+      const f32x16 s1 = qk(buf, 1);
+      __builtin_amdgcn_s_setprio(0);
+      consume(s0, s1, buf, kt * kBK);
+    };
+    for (int pr = 0; pr < n_pairs; ++pr) {
+      step(2 * pr, sk[1], sv[1]);
+      step(2 * pr + 1, sk[0], sv[0]);
+    }
   }
 
   // ---- epilogue: O = O^T / l, rows of 4 consecutive dims per store
