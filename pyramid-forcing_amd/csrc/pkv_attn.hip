@@ -8,10 +8,16 @@
 // workgroup per CU, so every SIMD runs two waves (each within 256 registers)
 // whose MFMA and softmax phases interleave.  All 512 threads stage both K and
 // V: 16-byte buffer loads bounded at the sequence's last row (rows past the
-// end read as zero), issued two tiles ahead, stored row-major into LDS with
-// 16-byte stores.  Each staged tile serves 256 query rows, which halves the
-// load and LDS-store traffic per flop of a 128-row workgroup.  The order of
-// the work items balances the XCDs (balanced_item).
+// end read as zero), issued two iterations before their store, stored
+// row-major into LDS with 16-byte stores.  Each staged tile serves 256 query
+// rows, which halves the load and LDS-store traffic per flop of a 128-row
+// workgroup.  The order of the work items balances the XCDs (balanced_item).
+//
+// Software pipelining.  Iteration j computes S(j+1) = K(j+1) Q^T while the
+// softmax of S(j), computed one iteration earlier, runs in the same basic
+// block, then O += V(j)^T P(j).  K and V tiles therefore sit in LDS one tile
+// apart (K(j+1) and V(j) during iteration j), in separate double buffers,
+// still with one barrier per tile.
 //
 // Operand arrangement.  The wave computes S^T = K * Q^T (A = K rows read
 // from LDS, B = Q^T kept in registers), so the 32x32 MFMA result gives every
@@ -249,41 +255,14 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
   // within one tile whatever the sequence length
   const int64_t row_elems = p.kv_tok;
   const int row_bytes = static_cast<int>(row_elems) * 2;
-  // two register sets: tile t is loaded into set t%2 two iterations before
-  // it is stored, so each load has two tile-times to arrive
+  // Two register sets of staged K and V rows; see the loop below for which
+  // tiles they hold.  A tile at or past the sequence's end gets a resource
+  // with no records: its loads return zero without touching memory, so every
+  // tile is loaded unconditionally (no branch around a load keeps the
+  // compiler's outstanding-load accounting exact, and each wait covers only
+  // the rows that are about to be stored).
   uint4 sk[2][LD], sv[2][LD];
-  // A tile at or past the sequence's end gets a resource with no records:
-  // its loads return zero without touching memory, so the loop can load
-  // every tile unconditionally (no branch around a load keeps the compiler's
-  // outstanding-load accounting exact, and each wait covers only the tile
-  // that is about to be stored).
-  auto load_tile = [&](int kt, uint4 (&k4)[LD], uint4 (&v4)[LD]) {
-    const int64_t first = static_cast<int64_t>(kt) * kBK;
-    const int64_t left = (static_cast<int64_t>(Lk) - first) * row_elems * 2;
-    const int nrec = static_cast<int>(left <= 0 ? 0 : (left < 0x7fffffff ? left : 0x7fffffff));
-    const int64_t base = left <= 0 ? 0 : first * row_elems;
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kp + base), 0, nrec, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vp + base), 0, nrec, kRsrcWord3);
-#pragma unroll
-    for (int r = 0; r < LD; ++r) {
-      const int idx = tid + r * kThreads;
-      const int off = (idx / KCH) * row_bytes + (idx % KCH) * 16;
-      k4[r] = bload16(rk, off);
-      v4[r] = bload16(rv, off);
-    }
-  };
-  auto store_tile = [&](int buf, const uint4 (&k4)[LD], const uint4 (&v4)[LD]) {
-#pragma unroll
-    for (int r = 0; r < LD; ++r) {
-      const int idx = tid + r * kThreads;
-      *reinterpret_cast<uint4 *>(&Ks[buf][(idx / KCH) * RS + (idx % KCH) * 8]) = k4[r];
-      *reinterpret_cast<uint4 *>(&Vs[buf][(idx / KCH) * RSV + (idx % KCH) * 8]) = v4[r];
-    }
-  };
-
-  // S^T for the 32 keys kb*32.. of the tile in buf
+  // S^T for the 32 keys kb*32.. of the K tile in buf
   auto qk = [&](int buf, int kb) {
     f32x16 acc;
 #pragma unroll
@@ -301,98 +280,129 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
   const int v_row = 4 * hf + ((lane & 15) >> 2);
   const int v_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  // softmax of one 64-key tile (two 32-key S^T blocks) and O^T += V^T P^T
-  auto consume = [&](f32x16 s0, f32x16 s1, int buf, int kb0) {
-    if (kb0 + kBK > Lk) {
+  // resource for the rows of tile kt of a K or V sequence
+  auto tile_rsrc = [&](const uint16_t *seq_base, int kt) {
+    const int64_t first = static_cast<int64_t>(kt) * kBK;
+    const int64_t left = (static_cast<int64_t>(Lk) - first) * row_elems * 2;
+    const int nrec = static_cast<int>(left <= 0 ? 0 : (left < 0x7fffffff ? left : 0x7fffffff));
+    const int64_t base = left <= 0 ? 0 : first * row_elems;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(seq_base + base), 0, nrec, kRsrcWord3);
+  };
+  auto load_rows = [&](const uint16_t *seq_base, int kt, uint4 (&x4)[LD]) {
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(seq_base, kt);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kb0 + 8 * (i / 4) + 4 * hf + (i % 4);
-        if (key >= Lk) s0[i] = -INFINITY;
-        if (key + 32 >= Lk) s1[i] = -INFINITY;
-      }
+    for (int i = 0; i < LD; ++i) {
+      const int idx = tid + i * kThreads;
+      x4[i] = bload16(r, (idx / KCH) * row_bytes + (idx % KCH) * 16);
     }
-    // maximum and sum as 4-way trees, not one serial chain each
-    float mq[4];
+  };
+  auto load_k = [&](int kt, uint4 (&k4)[LD]) { load_rows(kp, kt, k4); };
+  auto load_v = [&](int kt, uint4 (&v4)[LD]) { load_rows(vp, kt, v4); };
+  auto store_k = [&](int buf, const uint4 (&k4)[LD]) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      mq[r] = fmaxf(s0[r], s1[r]);
-#pragma unroll
-      for (int i = r + 4; i < 16; i += 4) mq[r] = fmaxf(mq[r], fmaxf(s0[i], s1[i]));
+    for (int r = 0; r < LD; ++r) {
+      const int idx = tid + r * kThreads;
+      *reinterpret_cast<uint4 *>(&Ks[buf][(idx / KCH) * RS + (idx % KCH) * 8]) = k4[r];
     }
-    float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
-    mx = half_max(mx) * c;
-    const bool move = mx > m + kLazy || m == -INFINITY;
-    float alpha = 1.0f;
-    if (move) {
-      alpha = __builtin_amdgcn_exp2f(m - mx);
-      m = mx;
+  };
+  auto store_v = [&](int buf, const uint4 (&v4)[LD]) {
+#pragma unroll
+    for (int r = 0; r < LD; ++r) {
+      const int idx = tid + r * kThreads;
+      *reinterpret_cast<uint4 *>(&Vs[buf][(idx / KCH) * RSV + (idx % KCH) * 8]) = v4[r];
     }
-    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    bf16x8 pb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float sv_ = ks < 2 ? s0[8 * ks + j] : s1[8 * (ks - 2) + j];
-        const float e = __builtin_amdgcn_exp2f(fmaf(sv_, c, -m));
-        ps[j & 3] += e;
-        pb[ks][j] = static_cast<__bf16>(e);
-      }
-    l = l * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
-    if (__any(move)) {
-      // in place (tied operands), so the accumulators keep their registers
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) asm volatile("v_mul_f32_e32 %0, %1, %0" : "+v"(o[db][i]) : "v"(alpha));
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint16_t *vptr = &Vs[buf][(16 * ks + v_row) * RSV + db * 32 + v_col];
-        const i16x4 lo = lds_tr16(vptr), hi = lds_tr16(vptr + 8 * RSV);
-        const i16x4 a8[2] = {lo, hi};
-        const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
-      }
   };
 
-  // The loop runs whole pairs of tiles: with an odd tile count the last
-  // step sees a tile wholly past the end, whose keys are all masked and
-  // which adds nothing to O or l.
   const int n_pairs = (Lk + 2 * kBK - 1) / (2 * kBK);
   if (n_pairs > 0) {
-    // the issue order tile 1 then tile 2 is kept (scheduling barriers), so
-    // that on entering the loop the loads of tile 1 are older than those of
-    // tile 2, as they are on every later iteration, and the first store of
-    // the loop waits for tile 1's loads only
-    load_tile(0, sk[0], sv[0]);
-    store_tile(0, sk[0], sv[0]);
+    // prologue: K0 -> Ks[0], V0 -> Vs[0], K1 -> Ks[1]; register set 0
+    // holds (K2, V1), set 1 (K3, V2); S(0) from Ks[0]
+    load_k(0, sk[0]);
+    load_v(0, sv[0]);
+    store_k(0, sk[0]);
+    store_v(0, sv[0]);
+    load_k(1, sk[1]);
+    store_k(1, sk[1]);
     __builtin_amdgcn_sched_barrier(0);
-    load_tile(1, sk[1], sv[1]);
+    load_k(2, sk[0]);
+    load_v(1, sv[0]);
     __builtin_amdgcn_sched_barrier(0);
-    load_tile(2, sk[0], sv[0]);
+    load_k(3, sk[1]);
+    load_v(2, sv[1]);
     __builtin_amdgcn_sched_barrier(0);
-    // iteration kt: tile kt is in LDS buffer kt%2; tile kt+1 (register set
-    // (kt+1)%2) is stored into the other buffer, then tile kt+3 is loaded
-    // into the set just freed
-    auto step = [&](int kt, uint4 (&k4)[LD], uint4 (&v4)[LD]) {
-      const int buf = kt & 1;
-      __syncthreads();  // tile kt visible; every wave is done with buffer buf^1
-      store_tile(buf ^ 1, k4, v4);
-      load_tile(kt + 3, k4, v4);
-      // the QK^T MFMA cluster runs at raised wave priority, so a wave that
-      // reaches it issues ahead of its SIMD partner's softmax VALU work
-      __builtin_amdgcn_s_setprio(2);
-      const f32x16 s0 = qk(buf, 0);
-      const f32x16 s1 = qk(buf, 1);
-      __builtin_amdgcn_s_setprio(0);
-      consume(s0, s1, buf, kt * kBK);
+    __syncthreads();
+    f32x16 sa0 = qk(0, 0), sa1 = qk(0, 1), sb0, sb1;
+
+    // iteration j: Ks[(j+1)%2] = K(j+1), Vs[j%2] = V(j), (c0, c1) = S(j);
+    // register set j%2 holds (K(j+2), V(j+1)), stored now, then refilled
+    // with (K(j+4), V(j+3)); S(j+1) is computed while S(j) goes through the
+    // softmax, then O += V(j)^T P(j)
+    auto step = [&](int j, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1, uint4 (&k4)[LD],
+                    uint4 (&v4)[LD]) {
+      __syncthreads();
+      store_k(j & 1, k4);
+      store_v((j + 1) & 1, v4);
+      load_k(j + 4, k4);
+      load_v(j + 3, v4);
+      const int kb0 = j * kBK;
+      if (kb0 + kBK > Lk) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb0 + 8 * (i / 4) + 4 * hf + (i % 4);
+          if (key >= Lk) c0[i] = -INFINITY;
+          if (key + 32 >= Lk) c1[i] = -INFINITY;
+        }
+      }
+      float mq[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        mq[r] = fmaxf(c0[r], c1[r]);
+#pragma unroll
+        for (int i = r + 4; i < 16; i += 4) mq[r] = fmaxf(mq[r], fmaxf(c0[i], c1[i]));
+      }
+      float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
+      mx = half_max(mx) * c;
+      const bool move = mx > m + kLazy || m == -INFINITY;
+      const float m_new = move ? mx : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      if (__any(move)) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) asm volatile("v_mul_f32_e32 %0, %1, %0" : "+v"(o[db][i]) : "v"(alpha));
+      }
+      // ---- one block: S(j+1) MFMAs interleaved with the exponentials of S(j)
+      n0 = qk((j + 1) & 1, 0);
+      n1 = qk((j + 1) & 1, 1);
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      bf16x8 pb[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float sv_ = ks < 2 ? c0[8 * ks + jj] : c1[8 * (ks - 2) + jj];
+          const float e = __builtin_amdgcn_exp2f(fmaf(sv_, c, -m));
+          ps[jj & 3] += e;
+          pb[ks][jj] = static_cast<__bf16>(e);
+        }
+      l = l * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      // ---- O^T += V(j)^T P(j)^T
+      const int vb = j & 1;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const uint16_t *vptr = &Vs[vb][(16 * ks + v_row) * RSV + db * 32 + v_col];
+          const i16x4 lo = lds_tr16(vptr), hi = lds_tr16(vptr + 8 * RSV);
+          const i16x4 a8[2] = {lo, hi};
+          const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
+        }
     };
     for (int pr = 0; pr < n_pairs; ++pr) {
-      step(2 * pr, sk[1], sv[1]);
-      step(2 * pr + 1, sk[0], sv[0]);
+      step(2 * pr, sa0, sa1, sb0, sb1, sk[0], sv[0]);
+      step(2 * pr + 1, sb0, sb1, sa0, sa1, sk[1], sv[1]);
     }
   }
 
