@@ -270,12 +270,24 @@ __device__ void route_head(HeadState &s, int h, int F, int64_t t0, int pass_kind
 // safe whatever slots the new frames land in.
 constexpr int kScatTok = 16;
 constexpr int kScatBatch = 4;  // frames (and shifted slots) staged per batch
-__global__ void __launch_bounds__(256) scatter_kernel(FrameSrc src, PosSrc pos, PoolPtrs pools, Workspace ws,
-                                                      int layer, int H, int F, int FSEQ, int D, int max_sink,
-                                                      int max_middle, int max_recent) {
-  const int h = blockIdx.y;
+struct ScatterArgs {
+  FrameSrc src;
+  PosSrc pos;
+  PoolPtrs pools;
+  Workspace ws;
+  int layer, H, F, FSEQ, D, max_sink, max_middle, max_recent;
+};
+
+// tile bx of head h (kScatTok tokens)
+__device__ void scatter_body(const ScatterArgs &sa, int bx, int h) {
+  const FrameSrc &src = sa.src;
+  const PosSrc &pos = sa.pos;
+  const PoolPtrs &pools = sa.pools;
+  const Workspace &ws = sa.ws;
+  const int layer = sa.layer, H = sa.H, F = sa.F, FSEQ = sa.FSEQ, D = sa.D;
+  const int max_sink = sa.max_sink, max_middle = sa.max_middle, max_recent = sa.max_recent;
   const Route r = ws.route[h];
-  const int tok0 = blockIdx.x * kScatTok;
+  const int tok0 = bx * kScatTok;
   const int cpt = D / 8;
   const int64_t lh = static_cast<int64_t>(layer) * H + h;
   const int64_t slot_elems = static_cast<int64_t>(FSEQ) * D;
@@ -385,6 +397,8 @@ __global__ void __launch_bounds__(256) scatter_kernel(FrameSrc src, PosSrc pos, 
     }
   }
 }
+
+__global__ void __launch_bounds__(256) scatter_kernel(ScatterArgs sa) { scatter_body(sa, blockIdx.x, blockIdx.y); }
 
 // ---------------------------------------------------------------------------
 // Veil merge accumulator (mega_merge_accum.cu:52-252)
@@ -532,18 +546,23 @@ constexpr int kMaxMergeSlots = 8;
 // One workgroup per head, frames in order.  All descriptors and running
 // weight sums are read in one round trip; the group lists built for a block
 // stay in LDS for the later frames of that block in the same call.
-__global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) {
-  extern __shared__ int32_t smem[];
-  int32_t *gid = smem;                                    // [FSEQ]
-  int32_t *members = gid + a.FSEQ;                        // [FSEQ]
-  int32_t *gstart = members + a.FSEQ;                     // [kMaxMergeGroups + 1]
-  int32_t *cntw = gstart + kMaxMergeGroups + 1;           // [kMergeWaves * kMaxMergeGroups]
-  int32_t *part = cntw + kMergeWaves * kMaxMergeGroups;   // [kMergeThreads]
+// LDS words merge_prep_body uses: group ids and member lists [FSEQ] each,
+// group starts [MTPA + 1], per-wave counts [kMergeWaves * MTPA] (a group
+// count never exceeds MTPA), scan partials [kMergeThreads]
+__host__ __device__ inline int64_t merge_prep_lds_words(int FSEQ, int MTPA) {
+  return 2 * static_cast<int64_t>(FSEQ) + (1 + kMergeWaves) * static_cast<int64_t>(MTPA) + 1 + kMergeThreads;
+}
+
+__device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
+  int32_t *gid = smem;
+  int32_t *members = gid + a.FSEQ;
+  int32_t *gstart = members + a.FSEQ;
+  int32_t *cntw = gstart + a.MTPA + 1;
+  int32_t *part = cntw + kMergeWaves * a.MTPA;
   __shared__ int32_t s_desc[kMaxMergeFrames][4];
   __shared__ float s_wsum[kMaxMergeSlots];
   __shared__ int32_t s_ng[kMaxMergeSlots];
   __shared__ int32_t s_maxy, s_maxx;
-  const int h = blockIdx.x;
   const int tid = threadIdx.x;
   const int MTPA = a.MTPA;
   const int32_t bf = a.states[h].block_frames;
@@ -652,6 +671,26 @@ __global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) 
     }
     __syncthreads();
   }
+}
+
+__global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) {
+  extern __shared__ int32_t smem[];
+  merge_prep_body(a, blockIdx.x, smem);
+}
+
+// The scatter of one update (blocks [0, n_scatter), gx tiles per head) and
+// its merge preparation (the next H blocks) touch disjoint memory, so they
+// share one launch and overlap: the latency-bound per-head merge work runs
+// beside the bandwidth-bound scatter.
+static_assert(kMergeThreads == 256, "scatter and merge prep share the block size");
+__global__ void __launch_bounds__(256) scatter_merge_prep_kernel(ScatterArgs sa, MergeArgs ma, int gx,
+                                                                  int n_scatter) {
+  extern __shared__ int32_t smem[];
+  const int b = blockIdx.x;
+  if (b < n_scatter)
+    scatter_body(sa, b % gx, b / gx);
+  else
+    merge_prep_body(ma, b - n_scatter, smem);
 }
 
 // Workgroup = (range of kGroupsPerWg groups, head); thread = (group, 8-wide
@@ -828,7 +867,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
   }
 }
 
-static int launch_merge(const MergeArgs &ma, hipStream_t st) {
+static int check_merge(const MergeArgs &ma) {
   if (ma.FSEQ > kMaxMergeFseq)
     return fail(PKV_ERR_UNSUPPORTED, "merge_accum: frame_seqlen %d exceeds %d", ma.FSEQ, kMaxMergeFseq);
   if (ma.MTPA > kMaxMergeGroups)
@@ -838,18 +877,33 @@ static int launch_merge(const MergeArgs &ma, hipStream_t st) {
     return fail(PKV_ERR_UNSUPPORTED, "merge_accum: %d frames per call exceed %d", ma.F, kMaxMergeFrames);
   if (ma.MMA > kMaxMergeSlots)
     return fail(PKV_ERR_UNSUPPORTED, "merge_accum: %d active merge blocks exceed %d", ma.MMA, kMaxMergeSlots);
-  const size_t smem = (2 * static_cast<size_t>(ma.FSEQ) + (1 + kMergeWaves) * kMaxMergeGroups + 1 + kMergeThreads) *
-                      sizeof(int32_t);
+  return PKV_OK;
+}
+
+// dynamic LDS of the merge preparation; above 64 KB the kernel must be
+// allowed to use it first
+static int merge_prep_smem(const MergeArgs &ma, const void *kernel, size_t &smem) {
+  smem = static_cast<size_t>(merge_prep_lds_words(ma.FSEQ, ma.MTPA)) * sizeof(int32_t);
   if (smem > 65536 &&
-      hipFuncSetAttribute(reinterpret_cast<const void *>(merge_prep_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
+      hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
     return fail(PKV_ERR_HIP, "merge_accum: cannot reserve %zu bytes of LDS", smem);
-  hipLaunchKernelGGL(merge_prep_kernel, dim3(ma.H), dim3(kMergeThreads), smem, st, ma);
-  int rc = check_launch("merge_prep_kernel");
-  if (rc) return rc;
+  return PKV_OK;
+}
+
+static int launch_merge_accum(const MergeArgs &ma, hipStream_t st) {
   dim3 grid((ma.MTPA + kGroupsPerWg - 1) / kGroupsPerWg, ma.H);
   hipLaunchKernelGGL(merge_accum_kernel, grid, dim3(kMergeThreads), 0, st, ma);
   return check_launch("merge_accum_kernel");
+}
+
+static int launch_merge(const MergeArgs &ma, hipStream_t st) {
+  int rc = check_merge(ma);
+  if (rc) return rc;
+  size_t smem;
+  if ((rc = merge_prep_smem(ma, reinterpret_cast<const void *>(merge_prep_kernel), smem))) return rc;
+  hipLaunchKernelGGL(merge_prep_kernel, dim3(ma.H), dim3(kMergeThreads), smem, st, ma);
+  if ((rc = check_launch("merge_prep_kernel"))) return rc;
+  return launch_merge_accum(ma, st);
 }
 
 static PoolPtrs pool_ptrs(const pkv_geometry *g, const pkv_pools *p) {
@@ -981,39 +1035,44 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   if ((rc = check_launch("route_kernel"))) return rc;
   FrameSrc src{a->new_k, a->new_v, static_cast<int64_t>(FSEQ) * a->tok_stride, a->head_stride, a->tok_stride};
   PosSrc pos{nullptr, a->t0, a->spatial_width, H, FSEQ};
-  dim3 grid((FSEQ + kScatTok - 1) / kScatTok, H);
-  hipLaunchKernelGGL(scatter_kernel, grid, dim3(256), 0, st, src, pos, pool_ptrs(geo, pools), ws, a->layer,
-                     H, a->frames, FSEQ, D, geo->max_sink, geo->max_middle, geo->max_recent);
-  if ((rc = check_launch("scatter_kernel"))) return rc;
-  if (a->pass_kind == 1 && a->has_merge_head) {
-    const int64_t l = a->layer;
-    const int MMA = geo->max_merge_active, MMB = geo->max_merge_blocks, MTPA = geo->max_merge_tokens;
-    MergeArgs ma;
-    ma.states = reinterpret_cast<const HeadState *>(a->states_layer);
-    ma.src = src;
-    ma.pos = pos;
-    ma.desc_kind = ws.desc[0];
-    ma.desc_slot = ws.desc[4];
-    ma.desc_fin = ws.desc[6];
-    ma.desc_new = ws.desc[7];
-    ma.weights = nullptr;
-    ma.ml.accum_sum_k = pools->merge_accum_sum_k + l * H * MMA * MTPA * D;
-    ma.ml.accum_sum_v = pools->merge_accum_sum_v + l * H * MMA * MTPA * D;
-    ma.ml.accum_pos = pools->merge_accum_pos + l * H * MMA * MTPA * 3;
-    ma.ml.accum_group_ids = pools->merge_accum_group_ids + l * H * MMA * FSEQ;
-    ma.ml.accum_tokens_per_group = pools->merge_accum_tokens_per_group + l * H * MMA * MTPA;
-    ma.ml.accum_num_groups = pools->merge_accum_num_groups + l * H * MMA;
-    ma.ml.accum_weight_sum = nullptr;
-    ma.ml.merge_k = pools->merge_k + l * H * MMB * MTPA * D;
-    ma.ml.merge_v = pools->merge_v + l * H * MMB * MTPA * D;
-    ma.ml.merge_pos = pools->merge_pos + l * H * MMB * MTPA * 3;
-    ma.ml.merge_token_count = pools->merge_token_count + l * H * MMB;
-    ma.ws = carve_merge_ws(static_cast<char *>(a->workspace) + update_ws_bytes(H, a->frames), H, a->frames, FSEQ,
-                           MTPA);
-    ma.H = H; ma.F = a->frames; ma.FSEQ = FSEQ; ma.D = D; ma.MMA = MMA; ma.MMB = MMB; ma.MTPA = MTPA;
-    if ((rc = launch_merge(ma, st))) return rc;
+  ScatterArgs sa{src, pos, pool_ptrs(geo, pools), ws, a->layer, H, a->frames, FSEQ, D,
+                 geo->max_sink, geo->max_middle, geo->max_recent};
+  const int gx = (FSEQ + kScatTok - 1) / kScatTok;
+  if (!(a->pass_kind == 1 && a->has_merge_head)) {
+    hipLaunchKernelGGL(scatter_kernel, dim3(gx, H), dim3(256), 0, st, sa);
+    return check_launch("scatter_kernel");
   }
-  return PKV_OK;
+  const int64_t l = a->layer;
+  const int MMA = geo->max_merge_active, MMB = geo->max_merge_blocks, MTPA = geo->max_merge_tokens;
+  MergeArgs ma;
+  ma.states = reinterpret_cast<const HeadState *>(a->states_layer);
+  ma.src = src;
+  ma.pos = pos;
+  ma.desc_kind = ws.desc[0];
+  ma.desc_slot = ws.desc[4];
+  ma.desc_fin = ws.desc[6];
+  ma.desc_new = ws.desc[7];
+  ma.weights = nullptr;
+  ma.ml.accum_sum_k = pools->merge_accum_sum_k + l * H * MMA * MTPA * D;
+  ma.ml.accum_sum_v = pools->merge_accum_sum_v + l * H * MMA * MTPA * D;
+  ma.ml.accum_pos = pools->merge_accum_pos + l * H * MMA * MTPA * 3;
+  ma.ml.accum_group_ids = pools->merge_accum_group_ids + l * H * MMA * FSEQ;
+  ma.ml.accum_tokens_per_group = pools->merge_accum_tokens_per_group + l * H * MMA * MTPA;
+  ma.ml.accum_num_groups = pools->merge_accum_num_groups + l * H * MMA;
+  ma.ml.accum_weight_sum = nullptr;
+  ma.ml.merge_k = pools->merge_k + l * H * MMB * MTPA * D;
+  ma.ml.merge_v = pools->merge_v + l * H * MMB * MTPA * D;
+  ma.ml.merge_pos = pools->merge_pos + l * H * MMB * MTPA * 3;
+  ma.ml.merge_token_count = pools->merge_token_count + l * H * MMB;
+  ma.ws = carve_merge_ws(static_cast<char *>(a->workspace) + update_ws_bytes(H, a->frames), H, a->frames, FSEQ,
+                         MTPA);
+  ma.H = H; ma.F = a->frames; ma.FSEQ = FSEQ; ma.D = D; ma.MMA = MMA; ma.MMB = MMB; ma.MTPA = MTPA;
+  if ((rc = check_merge(ma))) return rc;
+  size_t smem;
+  if ((rc = merge_prep_smem(ma, reinterpret_cast<const void *>(scatter_merge_prep_kernel), smem))) return rc;
+  hipLaunchKernelGGL(scatter_merge_prep_kernel, dim3(gx * H + H), dim3(256), smem, st, sa, ma, gx, gx * H);
+  if ((rc = check_launch("scatter_merge_prep_kernel"))) return rc;
+  return launch_merge_accum(ma, st);
 }
 
 }  // extern "C"
