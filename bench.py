@@ -34,6 +34,17 @@ PEAK_HBM_GBS = 8000.0
 FSEQ, H, L, D, QTOK = 1560, 12, 30, 128, 4680
 ATTN_KERNEL = "attn_fwd_kernel<128>"
 
+# HBM bytes per launch of each workload's dominant kernel, from two rocprofv3
+# --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) of
+# `bench.py --workload {attn,cache,merge}`, each scaled by what the same
+# counter reads for a 1 GiB device-to-device copy (FETCH_SIZE x 2.000,
+# WRITE_SIZE x 1.000); profiles/hbm_traffic_counters.md lists the runs.
+TRAFFIC_BYTES = {
+    "attn_fwd_kernel<128>": 5677.57e6 + 431.31e6,   # config 2, one launch (30 x 12 sequences)
+    "pack_kernel": 298.69e6 + 296.94e6,             # config 3, one layer call (mean over 273 launches)
+    "merge_accum_kernel": 13.71e6 + 5.70e6,         # config 4, one eviction (mean over 200 launches)
+}
+
 
 def config2_lengths(seed: int = 0):
     """Seeded label matrix and per-(layer, head) KV lengths (tokens)."""
@@ -467,7 +478,7 @@ def main():
                    "q_tokens_per_head": QTOK, "kv_tokens_mean": round(r["mean_lk"], 1),
                    "kv_tokens_total": int(r["lk"].sum()), "labels_seed": 0, "flop_per_step": r["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": TRAFFIC_BYTES[ATTN_KERNEL],
                      "kernel": ATTN_KERNEL, "avg_launch_ms": round(r["kernel_ms"], 4)},
     }
     if not args.no_cpu_baseline:
@@ -519,7 +530,8 @@ def secondary(args):
         "bytes_per_step": c3["total_bytes"], "update_bytes": c3["upd_bytes"], "pack_bytes": c3["pack_bytes"],
         "packed_tokens": c3["pack_tok"], "layers": L, "heads": H, "step": 40, "policy": "shipped best_labels.csv",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "dominant_kernel": "pack_kernel", "dominant_kernel_traffic": TRAFFIC_BYTES["pack_kernel"]},
         "plan_pack_layer0": {"ms": round(c3["plan_pack_ms_l0"], 4), "GB/s": round(pk_gbs, 2),
                              "frac": round(pk_gbs / PEAK_HBM_GBS, 4)},
         "parity_layer0_bit_exact": ok, "cpu_baseline": cpu}
@@ -531,7 +543,9 @@ def secondary(args):
         "value": round(gbs4, 2), "unit": "GB/s", "ms_per_step": round(c4["ms"], 4), "timing": "hip_graph_replay",
         "evictions_per_step": EVICTIONS, "bytes_per_step": c4["bytes"],
         "roofline": {"bound": "hbm", "achieved": round(gbs4, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs4 / PEAK_HBM_GBS, 4), "traffic": None},
+                     "frac": round(gbs4 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "dominant_kernel": "merge_accum_kernel",
+                     "dominant_kernel_traffic": TRAFFIC_BYTES["merge_accum_kernel"]},
         "parity_bit_exact": c4["parity"], "graph_replay_matches_eager": c4["graph_same"], "cpu_baseline": c4["cpu"]}
     return out
 

@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
                                                             const int64_t *vc, const int32_t *mtc,
                                                             pkv_plan_out o, int32_t *total_out) {
   __shared__ int32_t len[kMaxPlanPairs];
-  __shared__ int32_t part[kPlanThreads];
+  __shared__ int32_t part[1];
   __shared__ __attribute__((aligned(16))) HeadState s_states[kPlanStageHeads];
   __shared__ int64_t s_vc[kPlanStageHeads * 3];
   __shared__ int32_t s_mtc[kPlanStageHeads * kMaxMergeBlocks];
@@ -205,26 +205,33 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
     if ((tid & 63) == 0) len[q] = n;
   }
   __syncthreads();
-  // exclusive scan of len[0..pairs): contiguous chunk per thread, then a
-  // Hillis-Steele scan over the per-thread totals
-  const int per = (pairs + kPlanThreads - 1) / kPlanThreads;
-  const int q0 = tid * per, q1 = min(q0 + per, pairs);
-  int32_t acc = 0;
-  for (int q = q0; q < q1; ++q) acc += len[q];
-  part[tid] = acc;
+  // exclusive scan of len[0..pairs) in 64-pair chunks: each wave scans its
+  // chunks with lane shuffles, wave 0 scans the chunk totals, and every
+  // element gets its chunk's base (two barriers)
+  __shared__ int32_t ctot[kMaxPlanPairs / 64];
+  const int lane = tid & 63;
+  const int n_chunks = (pairs + 63) / 64;
+  for (int ch = wave; ch < n_chunks; ch += n_waves) {
+    const int q = ch * 64 + lane;
+    const int32_t v = q < pairs ? len[q] : 0;
+    const int32_t incl = wave_incl_sum(v, lane);
+    if (q < pairs) len[q] = incl - v;
+    if (lane == 63) ctot[ch] = incl;
+  }
   __syncthreads();
-  for (int off = 1; off < kPlanThreads; off <<= 1) {
-    const int32_t v = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
+  if (wave == 0) {
+    int32_t run = 0;
+    for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+      const int ch = c0 + lane;
+      const int32_t v = ch < n_chunks ? ctot[ch] : 0;
+      const int32_t incl = wave_incl_sum(v, lane);
+      if (ch < n_chunks) ctot[ch] = run + incl - v;
+      run += __shfl(incl, 63);
+    }
+    if (lane == 0) part[0] = run;
   }
-  int32_t base = part[tid] - acc;
-  for (int q = q0; q < q1; ++q) {
-    const int32_t l = len[q];
-    len[q] = base;
-    base += l;
-  }
+  __syncthreads();
+  for (int q = tid; q < pairs; q += blockDim.x) len[q] += ctot[q >> 6];
   __syncthreads();
   if (tid == 0) o.cu_seqlens_k[0] = 0;
   for (int q = wave; q < pairs; q += n_waves) {
@@ -233,7 +240,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
     const int32_t n = emit_pair<true>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, b, o);
     if ((tid & 63) == 0) o.cu_seqlens_k[q + 1] = b + n;
   }
-  if (tid == 0 && total_out) *total_out = part[kPlanThreads - 1];
+  if (tid == 0 && total_out) *total_out = part[0];
 }
 
 // ---------------------------------------------------------------------------
