@@ -469,6 +469,16 @@ static int plan_launch(const pkv_geometry *geo, const uint8_t *states_layer, con
                         ((geo->max_sink + geo->max_middle + geo->max_recent) * static_cast<int64_t>(geo->frame_seqlen) +
                          geo->max_merge_blocks * seg_max);
   if (bound > geo->max_pack_tokens) {
+    // the actual total needs a host read; a stream under graph capture
+    // cannot synchronise, so say why instead of invalidating the capture
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(PKV_ERR_UNSUPPORTED,
+                  "mega_plan_multi: %d chunks may pack up to %lld tokens, more than the pack workspace (%lld), "
+                  "and the actual total cannot be read back during graph capture: capture at most "
+                  "max_attend_chunks chunks with frame_seqlen >= max_merge_tokens (%d)",
+                  num_chunks, static_cast<long long>(bound), static_cast<long long>(geo->max_pack_tokens),
+                  geo->max_merge_tokens);
     int32_t total = 0;
     if (hipMemcpyAsync(&total, out->cu_seqlens_k + num_chunks * H, sizeof(int32_t), hipMemcpyDeviceToHost, st) !=
             hipSuccess ||
