@@ -439,14 +439,55 @@ def bench_merge(steps: int, warmup: int, seed: int = 0):
                                 f"oracle's C restatement, {cpu_s:.2f} s, single thread"))
 
 
+E2E_CHUNKS = 80  # 240 latent frames in chunks of 3 (about 60 s of video)
+
+
+def bench_e2e(chunks: int = E2E_CHUNKS, seed: int = 0):
+    """Config 5: the causal DiT rollout in the Wan2.1-T2V-1.3B shape with
+    random weights, cross-attention to a random 512 x 4096 text context, the
+    pyramid cache of a seeded 30 x 12 label matrix, 4 noisy denoising
+    forwards and one clean forward per 3-frame chunk.  Chunk 0 is warm-up;
+    the rest are timed with HIP events, and the pyramid path (cache update,
+    plan, pack, ragged self-attention) is timed by events around each
+    block's cache calls."""
+    import numpy as np
+    import torch
+
+    from pyramidkv import factory
+    from pyramidkv._mega_cache import build_mega_caches
+    from pyramidkv.causal_dit import CausalDiT, WanShape, rollout
+    from pyramidkv.rope import wan_freqs
+
+    shape = WanShape()
+    dev = "cuda:0"
+    model = CausalDiT(shape, dev, seed=seed)
+    labels = np.random.default_rng(seed).choice([-1, 1, 2], size=(shape.num_blocks, shape.heads)).tolist()
+    comps = factory.shipped_compositions(shape.num_blocks, shape.heads, labels=labels)
+    caches = build_mega_caches(shape.num_blocks, shape.heads, shape.head_dim, shape.frame_seqlen, MAX_SINK,
+                               MAX_MIDDLE, MAX_RECENT, comps, max_attend_chunks=3, device=dev,
+                               freqs=wan_freqs(shape.head_dim), spatial_width=shape.grid_w,
+                               spatial_height=shape.grid_h, **factory.PYRAMID_FORCING_REMAP)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    model.set_context(torch.randn(shape.text_len, shape.text_dim, generator=g, device=dev).to(torch.bfloat16))
+    r = rollout(model, caches, chunks, timed_from=1, seed=seed)
+    return {"value": round(r["chunks_per_s"], 3), "unit": "latent chunks/s", "ms_per_chunk": round(r["ms"] / r["chunks"], 2),
+            "chunks_timed": r["chunks"], "latent_frames": 3 * chunks, "forwards_per_chunk": r["forwards_per_chunk"],
+            "pyramid_path_ms_per_chunk": round(r["cache_ms"] / r["chunks"], 2),
+            "pyramid_path_share": round(r["cache_ms"] / r["ms"], 4),
+            "model": "random-init Wan2.1-T2V-1.3B shape (30 blocks, dim 1536, 12 heads, FFN 8960)",
+            "labels": "seeded 30x12 over {-1,1,2}", "text_context": "random 512x4096"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--headline-only", action="store_true", help="skip the config-3 / config-4 measurements")
-    ap.add_argument("--workload", choices=["all", "attn", "cache", "merge", "copy"], default="all",
+    ap.add_argument("--headline-only", action="store_true", help="skip the config-3 / 4 / 5 measurements")
+    ap.add_argument("--e2e-chunks", type=int, default=E2E_CHUNKS, help="3-frame chunks of the config-5 rollout")
+    ap.add_argument("--workload", choices=["all", "attn", "cache", "merge", "e2e", "copy"], default="all",
                     help="run one workload alone and print its timing (for profiler runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -492,7 +533,8 @@ def main():
 
 def single_workload(args):
     """One workload alone (no CPU legs), for rocprofv3 runs: attn = config-2
-    launches, cache = config-3 steps, merge = config-4 steps, copy = a
+    launches, cache = config-3 steps, merge = config-4 steps, e2e = the
+    config-5 rollout, copy = a
     device-to-device copy of 1 GiB (the reference kernel that calibrates the
     FETCH_SIZE / WRITE_SIZE counters: 1 GiB read + 1 GiB written)."""
     import torch
@@ -506,6 +548,8 @@ def single_workload(args):
     if args.workload == "merge":
         c4 = bench_merge(args.steps, args.warmup)
         return {"workload": "merge", "ms": c4["ms"], "bytes_per_step": c4["bytes"]}
+    if args.workload == "e2e":
+        return {"workload": "e2e", **bench_e2e(args.e2e_chunks)}
     src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(max(1, args.steps)):
@@ -547,6 +591,9 @@ def secondary(args):
                      "dominant_kernel": "merge_accum_kernel",
                      "dominant_kernel_traffic": TRAFFIC_BYTES["merge_accum_kernel"]},
         "parity_bit_exact": c4["parity"], "graph_replay_matches_eager": c4["graph_same"], "cpu_baseline": c4["cpu"]}
+    del c4
+    torch.cuda.empty_cache()
+    out["config5_e2e_rollout"] = bench_e2e(args.e2e_chunks)
     return out
 
 

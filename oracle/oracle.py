@@ -355,8 +355,10 @@ def attention_ref(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | No
 
 
 def ragged_attention_ref(q_flat, k_flat, v_flat, cu_q, cu_k, heads_q=1, kv_per_head=True, scale=None):
-    """q_flat [total_q, Hq, D]; k/v [total_k, D] (per-head ragged, sequence
-    b*Hq+h at cu_k[b*Hq+h]) -- float64 output [total_q, Hq, D]."""
+    """q_flat [total_q, Hq, D]; k/v [total_k, D] per-head ragged (sequence
+    b*Hq+h at cu_k[b*Hq+h]), or with kv_per_head=False one K/V sequence per
+    batch b at cu_k[b], as [total_k, D] shared by the heads or [total_k, Hq, D]
+    (flash_attn_varlen_func's layout) -- float64 output [total_q, Hq, D]."""
     out = np.zeros(q_flat.shape, np.float64)
     B = len(cu_q) - 1
     for b in range(B):
@@ -365,6 +367,8 @@ def ragged_attention_ref(q_flat, k_flat, v_flat, cu_q, cu_k, heads_q=1, kv_per_h
             q = q_flat[cu_q[b]:cu_q[b + 1], h]
             k = k_flat[cu_k[s]:cu_k[s + 1]]
             vv = v_flat[cu_k[s]:cu_k[s + 1]]
+            if k.ndim == 3:
+                k, vv = k[:, h], vv[:, h]
             out[cu_q[b]:cu_q[b + 1], h] = attention_ref(q, k, vv, scale)
     return out
 
