@@ -546,6 +546,30 @@ constexpr int kMaxMergeSlots = 8;
 // One workgroup per head, frames in order.  All descriptors and running
 // weight sums are read in one round trip; the group lists built for a block
 // stay in LDS for the later frames of that block in the same call.
+// Member lists of the arithmetic position grid (y = tok / W, x = tok % W,
+// the positions MegaCache.update gives its frames) when it tiles exactly
+// into patch x patch groups: group g = (gy, gx) holds the patch's tokens in
+// ascending order, so member slot i is token
+// (gy*patch + r/patch) * W + gx*patch + r%patch with g = i / patch^2,
+// r = i % patch^2, and gstart[g] = g * patch^2.  The same lists as the
+// stable CSR build, without its ballots and scans.
+__device__ inline bool grid_groups_regular(const PosSrc &pos, int patch, int MTPA) {
+  if (pos.pos || patch <= 0 || pos.width <= 0 || pos.FSEQ % pos.width != 0) return false;
+  const int rows_tok = pos.FSEQ / pos.width;
+  if (rows_tok % patch != 0 || pos.width % patch != 0) return false;
+  return (rows_tok / patch) * (pos.width / patch) <= MTPA;
+}
+
+__device__ inline void grid_groups_csr(const PosSrc &pos, int patch, int32_t *members, int32_t *gstart) {
+  const int W = pos.width, pp = patch * patch, cols = W / patch, ng = pos.FSEQ / pp;
+  for (int i = threadIdx.x; i < pos.FSEQ; i += blockDim.x) {
+    const int g = i / pp, r = i % pp;
+    members[i] = ((g / cols) * patch + r / patch) * W + (g % cols) * patch + r % patch;
+  }
+  for (int g = threadIdx.x; g <= ng; g += blockDim.x) gstart[g] = g * pp;
+  __syncthreads();
+}
+
 // LDS words merge_prep_body uses: group ids and member lists [FSEQ] each,
 // group starts [MTPA + 1], per-wave counts [kMergeWaves * MTPA] (a group
 // count never exceeds MTPA), scan partials [kMergeThreads]
@@ -630,7 +654,10 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
         if (a.ml.accum_weight_sum) a.ml.accum_weight_sum[hs] = 0.0f;
       }
       __syncthreads();
-      build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
+      if (grid_groups_regular(a.pos, patch, MTPA))
+        grid_groups_csr(a.pos, patch, members, gstart);
+      else
+        build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
       csr_slot = slot;
       float *tpg = a.ml.accum_tokens_per_group + hs * MTPA;
       for (int g = tid; g < MTPA; g += blockDim.x)
@@ -638,9 +665,13 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
     } else if (csr_slot != slot) {
       ng = s_ng[slot];
       if (ng > MTPA) ng = MTPA;
-      for (int t = tid; t < a.FSEQ; t += blockDim.x) gid[t] = gids_g[t];
-      __syncthreads();
-      build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
+      if (grid_groups_regular(a.pos, patch, MTPA) && ng == a.FSEQ / (patch * patch)) {
+        grid_groups_csr(a.pos, patch, members, gstart);
+      } else {
+        for (int t = tid; t < a.FSEQ; t += blockDim.x) gid[t] = gids_g[t];
+        __syncthreads();
+        build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
+      }
       csr_slot = slot;
     }
     // per-frame snapshot for the accumulation launch
