@@ -33,11 +33,16 @@
 // of O is lane-local.
 //
 // Softmax runs in the log2 domain (the scale is folded into one FMA before
-// v_exp_f32), keeps its running maximum per row and moves it only when a tile
-// exceeds it by more than kLazy: probabilities then stay <= 2^kLazy, far
-// inside fp32 and bf16 range, and the final O / l is the exact softmax.  P is
-// rounded to bf16 before the P*V product; row sums use the unrounded fp32
-// values (the flash-attention scheme).
+// v_exp_f32).  Fast pass: each query row's reference m is the maximum of its
+// first key tile and never moves, so the loop has no running maximum and O
+// is never rescaled; P = 2^(S*c - m) stays below 2^kHeadroom unless a later
+// key scores kHeadroom (log2 units) above the first tile.  A lane detects
+// that from its probability sums (a P at or above the bound makes its sum
+// reach it); the workgroup then recomputes its rows in a slow pass with the
+// classic moving maximum and rescaled O.  Either way the final O / l is the
+// exact softmax, with P rounded to bf16 for the P*V product and the row sums
+// taken over the same rounded values (v_dot2c_f32_bf16 against (1, 1)), so
+// numerator and denominator use identical weights.
 
 #include "pkv_common.h"
 
@@ -51,7 +56,7 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBK = 64;  // keys per LDS tile
-constexpr float kLazy = 8.0f;
+constexpr float kHeadroom = 64.0f;  // bound of log2(P) in the fast pass
 constexpr int kSchedMax = 1024;  // sequences the XCD-balanced schedule handles
 
 struct AttnParams {
@@ -178,6 +183,18 @@ __device__ inline float half_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// x + the sum of the 8 bf16 values of p (two accumulation chains)
+__device__ inline float bf16x8_sum(bf16x8 p, float x) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 one;
+  one[0] = static_cast<__bf16>(1.0f);
+  one[1] = one[0];
+  const bf16x2 p0 = {p[0], p[1]}, p1 = {p[2], p[3]}, p2 = {p[4], p[5]}, p3 = {p[6], p[7]};
+  const float a = __builtin_amdgcn_fdot2_f32_bf16(p0, one, x, false);
+  const float b = __builtin_amdgcn_fdot2_f32_bf16(p1, one, 0.0f, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(p3, one, __builtin_amdgcn_fdot2_f32_bf16(p2, one, a, false), false) + b;
+}
+
 __device__ inline float half_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -313,6 +330,56 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
     }
   };
 
+  // scores of keys past the sequence's end in the tile at key kb0 -> -inf
+  auto mask = [&](f32x16 &c0, f32x16 &c1, int kb0) {
+    if (kb0 + kBK > Lk) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb0 + 8 * (i / 4) + 4 * hf + (i % 4);
+        if (key >= Lk) c0[i] = -INFINITY;
+        if (key + 32 >= Lk) c1[i] = -INFINITY;
+      }
+    }
+  };
+  // the row maximum of a tile (scaled to the log2 domain)
+  auto tile_max = [&](const f32x16 &c0, const f32x16 &c1) {
+    float mq[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      mq[r] = fmaxf(c0[r], c1[r]);
+#pragma unroll
+      for (int i = r + 4; i < 16; i += 4) mq[r] = fmaxf(mq[r], fmaxf(c0[i], c1[i]));
+    }
+    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c;
+  };
+  // P = 2^(S*c - mr) as bf16 B operands (for each 16-key step, the lane's 8
+  // keys in the operand order); returns the lane's sum of its 32 P
+  auto probs = [&](const f32x16 &c0, const f32x16 &c1, float mr, bf16x8 (&pb)[4]) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const float sv_ = ks < 2 ? c0[8 * ks + jj] : c1[8 * (ks - 2) + jj];
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(sv_, c, -mr)));
+      }
+    return bf16x8_sum(pb[0], 0.0f) + bf16x8_sum(pb[2], bf16x8_sum(pb[1], 0.0f) + bf16x8_sum(pb[3], 0.0f));
+  };
+  // O^T += V^T P^T from V tile buffer vb
+  auto pv = [&](int vb, const bf16x8 (&pb)[4]) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const uint16_t *vptr = &Vs[vb][(16 * ks + v_row) * RSV + db * 32 + v_col];
+        const i16x4 lo = lds_tr16(vptr), hi = lds_tr16(vptr + 8 * RSV);
+        const i16x4 a8[2] = {lo, hi};
+        const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
+      }
+  };
+
+  __shared__ int ovf_any;
+  if (tid == 0) ovf_any = 0;
   const int n_pairs = (Lk + 2 * kBK - 1) / (2 * kBK);
   if (n_pairs > 0) {
     // prologue: K0 -> Ks[0], V0 -> Vs[0], K1 -> Ks[1]; register set 0
@@ -332,11 +399,14 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     f32x16 sa0 = qk(0, 0), sa1 = qk(0, 1), sb0, sb1;
+    mask(sa0, sa1, 0);
+    m = tile_max(sa0, sa1);  // finite: the first tile holds key 0
+    bool ovf = false;
 
     // iteration j: Ks[(j+1)%2] = K(j+1), Vs[j%2] = V(j), (c0, c1) = S(j);
     // register set j%2 holds (K(j+2), V(j+1)), stored now, then refilled
     // with (K(j+4), V(j+3)); S(j+1) is computed while S(j) goes through the
-    // softmax, then O += V(j)^T P(j)
+    // exponentials, then O += V(j)^T P(j)
     auto step = [&](int j, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1, uint4 (&k4)[LD],
                     uint4 (&v4)[LD]) {
       __syncthreads();
@@ -344,65 +414,52 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
       store_v((j + 1) & 1, v4);
       load_k(j + 4, k4);
       load_v(j + 3, v4);
-      const int kb0 = j * kBK;
-      if (kb0 + kBK > Lk) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kb0 + 8 * (i / 4) + 4 * hf + (i % 4);
-          if (key >= Lk) c0[i] = -INFINITY;
-          if (key + 32 >= Lk) c1[i] = -INFINITY;
-        }
-      }
-      float mq[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        mq[r] = fmaxf(c0[r], c1[r]);
-#pragma unroll
-        for (int i = r + 4; i < 16; i += 4) mq[r] = fmaxf(mq[r], fmaxf(c0[i], c1[i]));
-      }
-      float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
-      mx = half_max(mx) * c;
-      const bool move = mx > m + kLazy || m == -INFINITY;
-      const float m_new = move ? mx : m;
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      m = m_new;
-      if (__any(move)) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) asm volatile("v_mul_f32_e32 %0, %1, %0" : "+v"(o[db][i]) : "v"(alpha));
-      }
+      mask(c0, c1, j * kBK);
       // ---- one block: S(j+1) MFMAs interleaved with the exponentials of S(j)
       n0 = qk((j + 1) & 1, 0);
       n1 = qk((j + 1) & 1, 1);
-      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       bf16x8 pb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const float sv_ = ks < 2 ? c0[8 * ks + jj] : c1[8 * (ks - 2) + jj];
-          const float e = __builtin_amdgcn_exp2f(fmaf(sv_, c, -m));
-          ps[jj & 3] += e;
-          pb[ks][jj] = static_cast<__bf16>(e);
-        }
-      l = l * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
-      // ---- O^T += V(j)^T P(j)^T
-      const int vb = j & 1;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const uint16_t *vptr = &Vs[vb][(16 * ks + v_row) * RSV + db * 32 + v_col];
-          const i16x4 lo = lds_tr16(vptr), hi = lds_tr16(vptr + 8 * RSV);
-          const i16x4 a8[2] = {lo, hi};
-          const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ks], o[db], 0, 0, 0);
-        }
+      const float ps = probs(c0, c1, m, pb);
+      l += ps;
+      ovf |= !(ps < exp2f(kHeadroom));
+      pv(j & 1, pb);
     };
     for (int pr = 0; pr < n_pairs; ++pr) {
       step(2 * pr, sa0, sa1, sb0, sb1, sk[0], sv[0]);
       step(2 * pr + 1, sb0, sb1, sa0, sa1, sk[1], sv[1]);
+    }
+    if (ovf) ovf_any = 1;
+    __syncthreads();
+    if (ovf_any) {
+      // ---- slow pass: a later key outscored the first tile by kHeadroom.
+      // One tile at a time through buffer 0, online softmax with a moving
+      // maximum and O rescaled when it moves.
+      m = -INFINITY;
+      l = 0.0f;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+      for (int kt = 0; kt < 2 * n_pairs; ++kt) {
+        __syncthreads();
+        load_k(kt, sk[0]);
+        load_v(kt, sv[0]);
+        store_k(0, sk[0]);
+        store_v(0, sv[0]);
+        __syncthreads();
+        f32x16 c0 = qk(0, 0), c1 = qk(0, 1);
+        mask(c0, c1, kt * kBK);
+        const float m_new = fmaxf(m, tile_max(c0, c1));
+        const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+        m = m_new;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        bf16x8 pb[4];
+        l = l * alpha + probs(c0, c1, m, pb);
+        pv(0, pb);
+      }
     }
   }
 

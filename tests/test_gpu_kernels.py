@@ -277,6 +277,29 @@ def test_attention_vs_float64(case):
     assert err.max() < 2e-2 and err.mean() < 2e-3, (err.max(), err.mean())
 
 
+def test_attention_keys_outscoring_the_first_tile_vs_float64():
+    """The fast pass fixes each row's softmax reference at its first key tile.
+    Spiked keys later in the sequence score ~130 log2 units above it (past the
+    2^64 headroom: those workgroups recompute with a moving maximum) or ~33
+    (inside the headroom: the fast pass keeps them, with P up to 2^33); a spike
+    on the last key of a partial tile checks the masking on that path too."""
+    rng = np.random.default_rng(5)
+    H = 2
+    Lq, Lk = [300, 700], [[5000, 130], [2000, 64]]
+    q, k, v, cu_q, cu_k = _attn_case(rng, Lq, Lk, H)
+    q[:] = O.f32_to_bf16(np.ones(1, np.float32))[0]  # every score = 128 * mean(k row) * scale
+    for seq, pos, val in [(0, 4000, 8.0), (1, 100, 2.0), (2, 1999, 8.0)]:
+        k[cu_k[seq] + pos] = O.f32_to_bf16(np.full(128, val, np.float32))
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    out = torch.full_like(qd, float("nan"))
+    A.ragged_attn_fwd(qd, kd, vd, out, to_dev(cu_q), to_dev(cu_k), len(Lq), H, True, max(Lq), 128 ** -0.5)
+    got = O.bf16_to_f32(to_np(out)).astype(np.float64)
+    want = O.ragged_attention_ref(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), cu_q, cu_k, H, True)
+    err = np.abs(got - want)
+    assert np.isfinite(got).all()
+    assert err.max() < 2e-2 and err.mean() < 2e-3, (err.max(), err.mean())
+
+
 def test_attention_rejects_causal_and_bad_head_dim():
     q = torch.zeros(4, 1, 128, dtype=torch.bfloat16, device=DEV)
     cu = torch.tensor([0, 4], dtype=torch.int32, device=DEV)
