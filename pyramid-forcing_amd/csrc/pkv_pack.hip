@@ -287,6 +287,54 @@ __device__ inline uint4 rope_chunk(uint4 raw, int chunk, int64_t t, int64_t y, i
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// The table entry of complex pair e of a chunk: pairs [0, ft_cols) use the
+// t table, the next fy_cols the y table, the rest the x table; sel names
+// the coordinate (0 t, 1 y, 2 x) whose clamped row indexes it.
+struct PairTab {
+  const float *p;  // table base + 2 * column
+  int stride;      // floats per table row
+  int sel;
+};
+__device__ inline PairTab pair_tab(int chunk, int e, const Rope &r) {
+  const int pidx = chunk * 4 + e, fy_end = r.ft_cols + r.fy_cols;
+  if (pidx < r.ft_cols) return PairTab{r.ft + 2 * pidx, 2 * r.ft_cols, 0};
+  if (pidx < fy_end) return PairTab{r.fy + 2 * (pidx - r.ft_cols), 2 * r.fy_cols, 1};
+  return PairTab{r.fx + 2 * (pidx - fy_end), 2 * r.fx_cols, 2};
+}
+
+// f32 pair -> bf16x2 by the hardware round-to-nearest-even conversion, with
+// any NaN half replaced by 0x7fc0: the same bits as pack_bf16x2
+__device__ inline uint32_t cvt_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7fffu) > 0x7f80u) u = (u & 0xffff0000u) | 0x7fc0u;
+  if ((u & 0x7fff0000u) > 0x7f800000u) u = (u & 0xffffu) | 0x7fc00000u;
+  return u;
+}
+
+// rope_chunk with the table entries of the chunk's 4 pairs resolved
+// (tabs) and the clamped rows of the token's (t, y, x) given
+__device__ inline uint4 rope_chunk_rows(uint4 raw, const PairTab (&tabs)[4], const int (&rows)[3]) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float2 f[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = tabs[e].sel == 0 ? rows[0] : (tabs[e].sel == 1 ? rows[1] : rows[2]);
+    f[e] = *reinterpret_cast<const float2 *>(tabs[e].p + row * tabs[e].stride);
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float kr = bf16_to_f32(static_cast<uint16_t>(w[e] & 0xffff));
+    const float ki = bf16_to_f32(static_cast<uint16_t>(w[e] >> 16));
+    const float a = __fmul_rn(kr, f[e].x), b = __fmul_rn(ki, f[e].y);
+    const float c = __fmul_rn(kr, f[e].y), d = __fmul_rn(ki, f[e].x);
+    o[e] = cvt_bf16x2(__fsub_rn(a, b), __fadd_rn(c, d));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 __device__ inline uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 __device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
 // streaming store (non-temporal): the flat K/V of one layer call is larger
@@ -319,8 +367,17 @@ struct PackArgs {
 };
 
 __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
+  // clamped RoPE table rows (t, y, x) of the tile's tokens
+  __shared__ int s_rows[kPackTok][3];
   const int items = a.n_seg * a.tiles_per_seg;
   const int cpt = a.D / 8;
+  // when cpt divides the block, a thread handles one chunk index of every
+  // token it touches, so its 4 table entries are resolved once
+  const bool fixed_chunk = (kPackThreads % cpt) == 0;
+  PairTab tabs[4];
+  if (a.fuse && fixed_chunk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tabs[e] = pair_tab(threadIdx.x % cpt, e, a.rope);
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int seg = it / a.tiles_per_seg, tile = it % a.tiles_per_seg;
     const int kind = a.kind[seg];
@@ -340,13 +397,25 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     const int64_t *sp = a.pos[kind] ? a.pos[kind] + sg * stride * 3 : nullptr;
     uint16_t *ok = a.k_out + dst * a.D;
     uint16_t *ov = a.v_out + dst * a.D;
-    const bool rope = a.fuse && sp;
+    const bool rope = a.fuse && sp;  // uniform over the workgroup
     const int64_t tr = rope ? a.tremap[seg] : -1;
     // segments up to tiles_per_seg tiles long (every frame or merge anchor)
     // take one pass; longer ones are walked tiles_per_seg tiles at a time
     for (int tok0 = tile * kPackTok; tok0 < len; tok0 += a.tiles_per_seg * kPackTok) {
       const int ntok = min(kPackTok, len - tok0);
       const int n_items = ntok * cpt;
+      if (rope) {
+        // the tile's table rows, one thread per token (the positions are
+        // read once per token instead of once per chunk)
+        __syncthreads();  // the previous tile's readers are done
+        for (int i = threadIdx.x; i < ntok; i += blockDim.x) {
+          const int64_t *pp = sp + static_cast<int64_t>(tok0 + i) * 3;
+          s_rows[i][0] = clamp_row(tr >= 0 ? tr : pp[0], a.rope.ft_rows);
+          s_rows[i][1] = clamp_row(pp[1], a.rope.fy_rows);
+          s_rows[i][2] = clamp_row(pp[2], a.rope.fx_rows);
+        }
+        __syncthreads();
+      }
       // all of this thread's chunks of a round are loaded before any store
       // (up to kPackPer 16-byte K and V reads in flight per thread; one round
       // covers the tile for head_dim <= 128)
@@ -365,13 +434,19 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
         for (int u = 0; u < kPackPer; ++u) {
           const int i = base + threadIdx.x + u * kPackThreads;
           if (i >= n_items) continue;
-          const int tok = tok0 + i / cpt, ch = i % cpt;
-          const int64_t e = static_cast<int64_t>(tok) * a.D + ch * 8;
+          const int tl = i / cpt, ch = i % cpt;
+          const int64_t e = static_cast<int64_t>(tok0 + tl) * a.D + ch * 8;
           uint4 k4 = kk[u];
           if (rope) {
-            const int64_t *pp = sp + static_cast<int64_t>(tok) * 3;
-            const int64_t t = tr >= 0 ? tr : pp[0];
-            k4 = rope_chunk(k4, ch, t, pp[1], pp[2], a.rope);
+            const int rows[3] = {s_rows[tl][0], s_rows[tl][1], s_rows[tl][2]};
+            if (fixed_chunk) {
+              k4 = rope_chunk_rows(k4, tabs, rows);
+            } else {
+              PairTab t4[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) t4[q] = pair_tab(ch, q, a.rope);
+              k4 = rope_chunk_rows(k4, t4, rows);
+            }
           }
           st16_nt(ok + e, k4);
           st16_nt(ov + e, vv[u]);

@@ -100,6 +100,15 @@ def test_pack_with_rope_bit_exact(seed):
     for kv in ("k", "v"):
         arrays[f"merge_{kv}"] = O.f32_to_bf16(rng.standard_normal((L, H, 6, 420, 128)).astype(np.float32))
     arrays["merge_pos"] = rng.integers(0, 60, (L, H, 6, 420, 3)).astype(np.int64)
+    # special bf16 values in K: signed zeros, subnormals, the largest finite,
+    # infinities and NaNs (the rotated products then round through the same
+    # cases: overflow, subnormal results, NaN canonicalised to 0x7fc0)
+    special = np.array([0x0000, 0x8000, 0x0001, 0x807F, 0x0080, 0x7F7F, 0xFF7F, 0x7F80, 0xFF80, 0x7FC1, 0xFFC0,
+                        0x7F81], np.uint16)
+    for n in ("sink", "middle", "recent", "merge"):
+        flat = arrays[f"{n}_k"].reshape(-1)
+        at = rng.choice(flat.size, 4096, replace=False)
+        flat[at] = special[rng.integers(0, special.size, at.size)]
     dp.load(arrays)
     # random plan-shaped segment list over both layers
     n = 200
