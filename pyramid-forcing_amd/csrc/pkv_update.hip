@@ -425,11 +425,14 @@ struct MergeWs {  // one entry per (head, frame)
   int32_t *gstart;   // [H*F][MTPA+1]
   int32_t *ng;       // [H*F]
   float *wsum;       // [H*F]
+  int32_t *width;    // [H*F]: W > 0 when the groups are the regular patch grid
+                     // of a W-wide frame (members in closed form, no CSR
+                     // snapshot), 0 when members / gstart hold the lists
 };
 
 __host__ __device__ inline int64_t merge_ws_bytes(int H, int F, int FSEQ, int MTPA) {
   const int64_t n = static_cast<int64_t>(H) * F;
-  return align_up(n * FSEQ * 4, 256) + align_up(n * (MTPA + 1) * 4, 256) + 2 * align_up(n * 4, 256);
+  return align_up(n * FSEQ * 4, 256) + align_up(n * (MTPA + 1) * 4, 256) + 3 * align_up(n * 4, 256);
 }
 
 __host__ __device__ inline MergeWs carve_merge_ws(void *base, int H, int F, int FSEQ, int MTPA) {
@@ -443,6 +446,8 @@ __host__ __device__ inline MergeWs carve_merge_ws(void *base, int H, int F, int 
   w.ng = reinterpret_cast<int32_t *>(p);
   p += align_up(n * 4, 256);
   w.wsum = reinterpret_cast<float *>(p);
+  p += align_up(n * 4, 256);
+  w.width = reinterpret_cast<int32_t *>(p);
   return w;
 }
 
@@ -577,6 +582,36 @@ __host__ __device__ inline int64_t merge_prep_lds_words(int FSEQ, int MTPA) {
   return 2 * static_cast<int64_t>(FSEQ) + (1 + kMergeWaves) * static_cast<int64_t>(MTPA) + 1 + kMergeThreads;
 }
 
+// Width W of the regular patch grid that the group ids gid[0..FSEQ) form
+// (group of token t = ((t / W) / patch) * (W / patch) + (t % W) / patch,
+// the ids the grid positions y = t / W, x = t % W give), or 0.  W is where
+// the ids first fall back (the end of the first token row); every id is then
+// checked.  Grids one group wide have no such fall and report 0 (their
+// lists then come from the CSR build, which gives the same lists).
+__device__ int regular_grid_width(const int32_t *gid, int FSEQ, int patch, int ng) {
+  __shared__ int s_w, s_bad;
+  if (threadIdx.x == 0) {
+    s_w = FSEQ;
+    s_bad = 0;
+  }
+  __syncthreads();
+  if (patch > 0 && ng * patch * patch == FSEQ) {
+    int wl = FSEQ;
+    for (int t = 1 + threadIdx.x; t < FSEQ; t += blockDim.x)
+      if (gid[t] < gid[t - 1]) wl = min(wl, t);
+    if (wl < FSEQ) atomicMin(&s_w, wl);
+  }
+  __syncthreads();
+  const int W = s_w;
+  if (W >= FSEQ || W % patch != 0 || FSEQ % W != 0) return 0;
+  const int cols = W / patch;
+  bool bad = false;
+  for (int t = threadIdx.x; t < FSEQ; t += blockDim.x) bad |= gid[t] != ((t / W) / patch) * cols + (t % W) / patch;
+  if (bad) s_bad = 1;
+  __syncthreads();
+  return s_bad ? 0 : W;
+}
+
 __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
   int32_t *gid = smem;
   int32_t *members = gid + a.FSEQ;
@@ -586,7 +621,7 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
   __shared__ int32_t s_desc[kMaxMergeFrames][4];
   __shared__ float s_wsum[kMaxMergeSlots];
   __shared__ int32_t s_ng[kMaxMergeSlots];
-  __shared__ int32_t s_maxy, s_maxx;
+  __shared__ int32_t s_maxy, s_maxx, s_irregular;
   const int tid = threadIdx.x;
   const int MTPA = a.MTPA;
   const int32_t bf = a.states[h].block_frames;
@@ -604,7 +639,9 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
     s_ng[tid] = a.ml.accum_num_groups[hs];
   }
   __syncthreads();
-  int csr_slot = -1;  // slot whose group lists are in LDS
+  // The group lists of the slot last seen: its regular grid width (members
+  // in closed form), or its CSR in LDS (width 0)
+  int list_slot = -1, list_w = 0;
   int ng = 0;
   for (int f = 0; f < a.F; ++f) {
     const int di = h * a.F + f;
@@ -613,7 +650,11 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
     const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
     int32_t *gids_g = a.ml.accum_group_ids + hs * a.FSEQ;
     if (is_new) {
-      if (tid == 0) { s_maxy = -1; s_maxx = -1; }
+      if (tid == 0) {
+        s_maxy = -1;
+        s_maxx = -1;
+        s_irregular = 0;
+      }
       __syncthreads();
       int32_t my = -1, mx = -1;
       for (int t = tid; t < a.FSEQ; t += blockDim.x) {
@@ -630,6 +671,12 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
       const int32_t rows = (s_maxy >= 0 && patch > 0) ? (s_maxy / patch + 1) : 1;
       ng = rows * cols;
       if (ng > MTPA) ng = MTPA;
+      // the positions are the regular grid of a W-wide frame (W = max x + 1)
+      // when every token t sits at (t / W, t % W) and patch tiles the grid
+      const int32_t W = s_maxx + 1;
+      const bool grid_ok = patch > 0 && W > 0 && a.FSEQ % W == 0 && W % patch == 0 &&
+                           (a.FSEQ / W) % patch == 0 && ng == a.FSEQ / (patch * patch);
+      bool irregular = !grid_ok;
       for (int t = tid; t < a.FSEQ; t += blockDim.x) {
         int64_t pt, py, px;
         a.pos.get(f, h, t, pt, py, px);
@@ -638,7 +685,9 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
         if (g < 0 || g >= ng) g = 0;
         gid[t] = g;
         gids_g[t] = g;
+        irregular |= grid_ok && (py != t / W || px != t % W);
       }
+      if (irregular) s_irregular = 1;
       int64_t tpos, ty, tx;
       a.pos.get(f, h, 0, tpos, ty, tx);
       for (int g = tid; g < ng; g += blockDim.x) {
@@ -654,33 +703,38 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
         if (a.ml.accum_weight_sum) a.ml.accum_weight_sum[hs] = 0.0f;
       }
       __syncthreads();
-      if (grid_groups_regular(a.pos, patch, MTPA))
-        grid_groups_csr(a.pos, patch, members, gstart);
-      else
-        build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
-      csr_slot = slot;
+      list_slot = slot;
+      list_w = s_irregular ? 0 : W;
+      if (!list_w) build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
       float *tpg = a.ml.accum_tokens_per_group + hs * MTPA;
-      for (int g = tid; g < MTPA; g += blockDim.x)
-        tpg[g] = g < ng ? static_cast<float>(gstart[g + 1] - gstart[g]) * static_cast<float>(bf) : 0.0f;
-    } else if (csr_slot != slot) {
+      for (int g = tid; g < MTPA; g += blockDim.x) {
+        const int32_t cnt = list_w ? patch * patch : (g < ng ? gstart[g + 1] - gstart[g] : 0);
+        tpg[g] = g < ng ? static_cast<float>(cnt) * static_cast<float>(bf) : 0.0f;
+      }
+    } else if (list_slot != slot) {
       ng = s_ng[slot];
       if (ng > MTPA) ng = MTPA;
+      list_slot = slot;
       if (grid_groups_regular(a.pos, patch, MTPA) && ng == a.FSEQ / (patch * patch)) {
-        grid_groups_csr(a.pos, patch, members, gstart);
+        list_w = a.pos.width;  // the arithmetic positions of MegaCache.update
       } else {
         for (int t = tid; t < a.FSEQ; t += blockDim.x) gid[t] = gids_g[t];
         __syncthreads();
-        build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
+        list_w = regular_grid_width(gid, a.FSEQ, patch, ng);
+        if (!list_w) build_csr(gid, a.FSEQ, ng, cntw, gstart, members, part);
       }
-      csr_slot = slot;
     }
-    // per-frame snapshot for the accumulation launch
-    int32_t *wm = a.ws.members + static_cast<int64_t>(di) * a.FSEQ;
-    int32_t *wg = a.ws.gstart + static_cast<int64_t>(di) * (MTPA + 1);
-    for (int t = tid; t < a.FSEQ; t += blockDim.x) wm[t] = members[t];
-    for (int g = tid; g <= ng; g += blockDim.x) wg[g] = gstart[g];
+    // per-frame snapshot for the accumulation launch: the grid width, or
+    // the member lists
+    if (!list_w) {
+      int32_t *wm = a.ws.members + static_cast<int64_t>(di) * a.FSEQ;
+      int32_t *wg = a.ws.gstart + static_cast<int64_t>(di) * (MTPA + 1);
+      for (int t = tid; t < a.FSEQ; t += blockDim.x) wm[t] = members[t];
+      for (int g = tid; g <= ng; g += blockDim.x) wg[g] = gstart[g];
+    }
     if (tid == 0) {
       a.ws.ng[di] = ng;
+      a.ws.width[di] = list_w;
       float ws = 1.0f;
       if (a.weights && a.ml.accum_weight_sum) {
         ws = s_wsum[slot] + a.weights[f];
@@ -738,6 +792,7 @@ constexpr int kAccBatch = 8;          // member tokens loaded per batch
 __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a) {
   __shared__ int32_t s_desc[kMaxMergeFrames][4];
   __shared__ int32_t s_ng[kMaxMergeFrames];
+  __shared__ int32_t s_w[kMaxMergeFrames];  // regular grid width, 0: CSR lists
   __shared__ float s_wsum[kMaxMergeFrames];
   __shared__ int32_t s_gs[kMaxMergeFrames][kGroupsPerWg + 1];  // member-slice offsets (relative to s_off)
   __shared__ int32_t s_off[kMaxMergeFrames];
@@ -749,6 +804,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
   const int D = a.D, MTPA = a.MTPA;
   const int cpt = D / 8;
   const int32_t bf = a.states[h].block_frames;
+  const int32_t patch = a.states[h].patch_size;
   if (tid < a.F) {
     const int di = h * a.F + tid;
     const int kind = a.desc_kind[di], slot = a.desc_slot[di];
@@ -758,6 +814,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
     s_desc[tid][2] = a.desc_new[di];
     s_desc[tid][3] = a.desc_fin[di];
     s_ng[tid] = merge ? a.ws.ng[di] : 0;
+    s_w[tid] = merge ? a.ws.width[di] : 0;
     s_wsum[tid] = merge ? a.ws.wsum[di] : 1.0f;
   }
   __syncthreads();
@@ -768,9 +825,14 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
   }
   __syncthreads();
   if (s_nmerge == 0) return;
-  // group-range offsets of every merge frame (gstart is read from the
-  // frame's snapshot) and the total member count they span
-  if (tid < a.F && s_desc[tid][0]) {
+  // group-range offsets of every merge frame with CSR lists (gstart is read
+  // from the frame's snapshot) and the total member count they span; frames
+  // on the regular grid stage nothing
+  if (tid < a.F && s_desc[tid][0] && s_w[tid]) {
+    const int f = tid;
+    for (int j = 0; j <= kGroupsPerWg; ++j) s_gs[f][j] = 0;
+    s_off[f] = 0;
+  } else if (tid < a.F && s_desc[tid][0]) {
     const int f = tid;
     const int32_t *gstart = a.ws.gstart + static_cast<int64_t>(h * a.F + f) * (MTPA + 1);
     const int ng = s_ng[f];
@@ -831,8 +893,14 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
       if (is_new)
         for (int e = 0; e < 8; ++e) { ak[e] = 0.0f; av[e] = 0.0f; }
       const float w = a.weights ? a.weights[f] : 1.0f;
+      // members of group g: closed form on the regular grid of width W
+      // (ascending: rows of the patch, then columns), else the staged or
+      // snapshotted CSR slice
+      const int W = s_w[f];
+      const int gcols = W > 0 ? W / patch : 1;
+      const int gbase = W > 0 ? (g / gcols) * patch * W + (g % gcols) * patch : 0;
       if (g < ng) {
-        const int m0 = s_gs[f][gl], m1 = s_gs[f][gl + 1];
+        const int m0 = W > 0 ? 0 : s_gs[f][gl], m1 = W > 0 ? patch * patch : s_gs[f][gl + 1];
         const int32_t *gmem = a.ws.members + static_cast<int64_t>(h * a.F + f) * a.FSEQ + s_off[f];
         for (int mb = m0; mb < m1; mb += kAccBatch) {
           const int n = min(kAccBatch, m1 - mb);
@@ -840,7 +908,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
 #pragma unroll
           for (int b = 0; b < kAccBatch; ++b)
             if (b < n) {
-              const int tok = staged ? s_mem[fpos + mb + b] : gmem[mb + b];
+              const int m = mb + b;
+              const int tok = W > 0 ? gbase + (m / patch) * W + m % patch : (staged ? s_mem[fpos + m] : gmem[m]);
               const int64_t so = a.src.off(f, h, tok) + c;
               kk[b] = ld16(a.src.k + so);
               vv[b] = ld16(a.src.v + so);
@@ -871,7 +940,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
         }
       }
       if (fin >= 0 && fin < a.MMB && g < ng) {
-        const int32_t count = s_gs[f][gl + 1] - s_gs[f][gl];
+        const int32_t count = W > 0 ? patch * patch : s_gs[f][gl + 1] - s_gs[f][gl];
         const float div = a.weights ? static_cast<float>(count) * s_wsum[f]
                                     : static_cast<float>(count) * static_cast<float>(bf);
         const float inv = div > 0.0f ? 1.0f / div : 0.0f;

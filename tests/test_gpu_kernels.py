@@ -194,9 +194,12 @@ def test_update_frames_bit_exact():
         assert (dp.np(k) == w).all(), k
 
 
-def _merge_run(H, FSEQ, W, blocks_t, seed, weights=None):
-    """Drive consecutive calls through the state machine + merge on both sides."""
+def _merge_run(H, FSEQ, W, blocks_t, seed, weights=None, permute=False):
+    """Drive consecutive calls through the state machine + merge on both sides.
+    permute: token t sits at a shuffled grid cell instead of cell t (same cells, so the
+    same groups, but member lists that are not the row-major closed form)."""
     rng = np.random.default_rng(seed)
+    cell = rng.permutation(FSEQ) if permute else np.arange(FSEQ)
     D, MT = 128, 420
     states_host = O.states_to_bytes([O.make_merge(2, int(c)) for c in rng.integers(2, 7, H)])
     states_dev = to_dev(states_host)
@@ -214,8 +217,8 @@ def _merge_run(H, FSEQ, W, blocks_t, seed, weights=None):
         nv = O.f32_to_bf16(rng.standard_normal((F, H, FSEQ, D)).astype(np.float32))
         pos = np.zeros((F, H, FSEQ, 3), np.int64)
         pos[..., 0] = np.asarray(t_vals).reshape(F, 1, 1)
-        pos[..., 1] = np.arange(FSEQ) // W
-        pos[..., 2] = np.arange(FSEQ) % W
+        pos[..., 1] = cell // W
+        pos[..., 2] = cell % W
         w = None if weights is None else rng.uniform(0.1, 1.0, F).astype(np.float32)
         desc = O.state_update(states_host, t_vals, 1)
         O.merge_accum(states_host, nk, nv, pos, desc, acc, w)
@@ -247,6 +250,16 @@ def test_merge_irregular_grid_and_reuse_in_call():
     # finalizes a block and starts the next block in the freed slot
     blocks = [[5 * b + f for f in range(5)] for b in range(6)]
     _merge_run(H=2, FSEQ=7 * 9 + 3, W=7, blocks_t=blocks, seed=2)
+
+
+def test_merge_one_group_wide_and_permuted_grids():
+    # a grid one patch wide has no row wrap in its group ids (member lists
+    # from the CSR build); permuted cells keep the group sets but not the
+    # closed-form member order, in new blocks and in blocks continued across
+    # calls
+    blocks = [[3 * b + f for f in range(3)] for b in range(4)]
+    _merge_run(H=2, FSEQ=2 * 12, W=2, blocks_t=blocks, seed=4)
+    _merge_run(H=2, FSEQ=1560, W=52, blocks_t=blocks, seed=5, permute=True)
 
 
 def test_merge_weighted_bit_exact():
