@@ -332,6 +332,36 @@ typedef struct pkv_update_args {
 int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools,
                      const pkv_update_args *args, pkv_stream_t stream);
 
+/*
+ * Row operations of the causal DiT block around the cache, for the
+ * end-to-end rollout (replacing the eager PyTorch chains of
+ * wan/modules/model.py:70-99 WanRMSNorm / WanLayerNorm and the modulation
+ * and gated residuals of wan/modules/causal_model.py:395-420).  Rows are
+ * contiguous runs of `cols` values; one wave reduces one row in registers.
+ *
+ * pkv_dit_layer_norm: out[r] = bf16(LN(x[r]) * m + a), LN without affine
+ *   weights (biased variance, eps inside the square root); m = 1 + mul when
+ *   mul_plus_one (modulation: norm(x) * (1 + scale) + shift), else mul
+ *   (LayerNorm affine weight); mul and add may be NULL (1 and 0).  x fp32
+ *   [rows, cols], cols a multiple of 4 and at most 4096.
+ * pkv_dit_rms_norm: out[r] = bf16(x[r] * rsqrt(mean(x[r]^2) + eps) * w) in
+ *   fp32; x bf16 with a row stride (a column slice of a wider tensor),
+ *   cols and strides multiples of 8, cols at most 8192; weight may be NULL.
+ * pkv_dit_residual: x[r, c] += float(y[r, c]) * gate[c] in fp32 (gate may be
+ *   NULL), in place; x fp32 [rows, cols], y bf16 with a row stride.
+ * pkv_dit_gelu_tanh: out = bf16(gelu_tanh(float(x))) elementwise, n a
+ *   multiple of 8.
+ */
+int pkv_dit_layer_norm(const float *x, int64_t rows, int32_t cols, const float *mul,
+                       const float *add, int32_t mul_plus_one, float eps, uint16_t *out,
+                       pkv_stream_t stream);
+int pkv_dit_rms_norm(const uint16_t *x, int64_t x_row_stride, int64_t rows, int32_t cols,
+                     const float *weight, float eps, uint16_t *out, int64_t out_row_stride,
+                     pkv_stream_t stream);
+int pkv_dit_residual(float *x, int64_t rows, int32_t cols, const uint16_t *y,
+                     int64_t y_row_stride, const float *gate, pkv_stream_t stream);
+int pkv_dit_gelu_tanh(const uint16_t *x, int64_t n, uint16_t *out, pkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,250 @@
+// Row operations of the causal DiT block that drives the pyramid cache in the
+// end-to-end rollout (wan/modules/causal_model.py:395-420 of the reference):
+// LayerNorm with modulation or affine weights, RMSNorm of q and k
+// (wan/modules/model.py:70-99), the gated residual updates of the fp32
+// residual stream, and the tanh GELU of the feed-forward.  Each is one
+// launch instead of the chain of elementwise and reduction kernels that
+// eager PyTorch runs for it.
+//
+// The row kernels give one wave to a row: lane i holds the 16-byte vectors
+// i, i + 64, ... of the row in registers (up to kMaxVec of them), the sums
+// are wave reductions, and the row is read from memory once.  LayerNorm
+// takes the mean first and then the sum of squared deviations (two-pass in
+// registers), so a large mean does not cancel the variance.
+
+#include "pkv_common.h"
+
+namespace pkv {
+
+constexpr int kDitRowsPerBlock = 4;  // one wave per row
+constexpr int kMaxVec = 16;          // 16-byte vectors per lane: rows up to 4096 fp32 / 8192 bf16
+
+__device__ inline float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+__device__ inline float4 ld_f4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+// out[r, :] = bf16(LN(x[r, :]) * m + a), LN without affine weights; m =
+// (one_plus ? 1 + mul : mul) and a = add, each optional (1 and 0)
+template <int K>
+__global__ void __launch_bounds__(64 * kDitRowsPerBlock) ln_mod_kernel(const float *x, int64_t rows, int C,
+                                                                       const float *mul, const float *add,
+                                                                       int one_plus, float eps, uint16_t *out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kDitRowsPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float *xr = x + r * C;
+  const int nv = C / 4;
+  float4 v[K];
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int j = lane + 64 * k;
+    v[k] = j < nv ? ld_f4(xr + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+  }
+  const float mean = wave_sum(s) / static_cast<float>(C);
+  float q = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int j = lane + 64 * k;
+    if (j < nv) {
+      const float a = v[k].x - mean, b = v[k].y - mean, c = v[k].z - mean, d = v[k].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) / static_cast<float>(C) + eps);
+  uint16_t *orow = out + r * C;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int j = lane + 64 * k;
+    if (j >= nv) continue;
+    float y[4] = {(v[k].x - mean) * rstd, (v[k].y - mean) * rstd, (v[k].z - mean) * rstd, (v[k].w - mean) * rstd};
+    if (mul) {
+      const float4 m = ld_f4(mul + 4 * j);
+      const float mm[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] *= one_plus ? 1.0f + mm[e] : mm[e];
+    }
+    if (add) {
+      const float4 a = ld_f4(add + 4 * j);
+      y[0] += a.x;
+      y[1] += a.y;
+      y[2] += a.z;
+      y[3] += a.w;
+    }
+    *reinterpret_cast<uint2 *>(orow + 4 * j) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+  }
+}
+
+// out[r, :] = bf16(x * rsqrt(mean(x^2) + eps) * w) in fp32, x bf16
+template <int K>
+__global__ void __launch_bounds__(64 * kDitRowsPerBlock) rms_kernel(const uint16_t *x, int64_t x_stride, int64_t rows,
+                                                                    int C, const float *w, float eps,
+                                                                    uint16_t *out, int64_t out_stride) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kDitRowsPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const uint16_t *xr = x + r * x_stride;
+  const int nv = C / 8;
+  uint4 v[K];
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int j = lane + 64 * k;
+    v[k] = j < nv ? *reinterpret_cast<const uint4 *>(xr + 8 * j) : make_uint4(0, 0, 0, 0);
+    const uint32_t wd[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = bf16_to_f32(static_cast<uint16_t>(wd[e] & 0xffff));
+      const float b = bf16_to_f32(static_cast<uint16_t>(wd[e] >> 16));
+      s += a * a + b * b;
+    }
+  }
+  const float rn = rsqrtf(wave_sum(s) / static_cast<float>(C) + eps);
+  uint16_t *orow = out + r * out_stride;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int j = lane + 64 * k;
+    if (j >= nv) continue;
+    const uint32_t wd[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a = bf16_to_f32(static_cast<uint16_t>(wd[e] & 0xffff)) * rn;
+      float b = bf16_to_f32(static_cast<uint16_t>(wd[e] >> 16)) * rn;
+      if (w) {
+        a *= w[8 * j + 2 * e];
+        b *= w[8 * j + 2 * e + 1];
+      }
+      o[e] = pack_bf16x2(a, b);
+    }
+    *reinterpret_cast<uint4 *>(orow + 8 * j) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// x[r, c] += float(y[r, c]) * gate[c] (gate optional: 1), 4 columns per thread
+__global__ void __launch_bounds__(256) residual_kernel(float *x, int64_t rows, int C, const uint16_t *y,
+                                                       int64_t y_stride, const float *gate) {
+  const int nv = C / 4;
+  const int64_t total = rows * nv;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / nv;
+    const int j = static_cast<int>(i % nv);
+    float4 a = ld_f4(x + r * C + 4 * j);
+    const uint2 b = *reinterpret_cast<const uint2 *>(y + r * y_stride + 4 * j);
+    float yv[4] = {bf16_to_f32(static_cast<uint16_t>(b.x & 0xffff)), bf16_to_f32(static_cast<uint16_t>(b.x >> 16)),
+                   bf16_to_f32(static_cast<uint16_t>(b.y & 0xffff)), bf16_to_f32(static_cast<uint16_t>(b.y >> 16))};
+    if (gate) {
+      const float4 g = ld_f4(gate + 4 * j);
+      yv[0] *= g.x;
+      yv[1] *= g.y;
+      yv[2] *= g.z;
+      yv[3] *= g.w;
+    }
+    a.x += yv[0];
+    a.y += yv[1];
+    a.z += yv[2];
+    a.w += yv[3];
+    *reinterpret_cast<float4 *>(x + r * C + 4 * j) = a;
+  }
+}
+
+// out = bf16(0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3)))) in fp32, 8 values per thread
+__global__ void __launch_bounds__(256) gelu_tanh_kernel(const uint16_t *x, int64_t n8, uint16_t *out) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n8;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(x + 8 * i);
+    const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float f[2] = {bf16_to_f32(static_cast<uint16_t>(wd[e] & 0xffff)), bf16_to_f32(static_cast<uint16_t>(wd[e] >> 16))};
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float u = f[q];
+        f[q] = 0.5f * u * (1.0f + tanhf(0.7978845608028654f * (u + 0.044715f * u * u * u)));
+      }
+      o[e] = pack_bf16x2(f[0], f[1]);
+    }
+    *reinterpret_cast<uint4 *>(out + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+static int row_grid(int64_t rows) {
+  const int64_t g = (rows + kDitRowsPerBlock - 1) / kDitRowsPerBlock;
+  return static_cast<int>(g);
+}
+
+static int flat_grid(int64_t items) {
+  int64_t g = (items + 255) / 256;
+  if (g > 65536) g = 65536;
+  return static_cast<int>(g < 1 ? 1 : g);
+}
+
+}  // namespace pkv
+
+using namespace pkv;
+
+extern "C" int pkv_dit_layer_norm(const float *x, int64_t rows, int32_t cols, const float *mul, const float *add,
+                                  int32_t mul_plus_one, float eps, uint16_t *out, pkv_stream_t stream) {
+  if (rows == 0) return PKV_OK;
+  if (!x || !out || rows < 0 || cols <= 0) return fail(PKV_ERR_INVALID, "dit_layer_norm: bad arguments");
+  if (cols % 4) return fail(PKV_ERR_INVALID, "dit_layer_norm: cols (%d) must be a multiple of 4", cols);
+  if (rows > 0x7fffffffLL * kDitRowsPerBlock) return fail(PKV_ERR_UNSUPPORTED, "dit_layer_norm: too many rows");
+  const int vec = (cols / 4 + 63) / 64;
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(row_grid(rows)), block(64 * kDitRowsPerBlock);
+  if (vec <= 4)
+    hipLaunchKernelGGL(ln_mod_kernel<4>, grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out);
+  else if (vec <= 8)
+    hipLaunchKernelGGL(ln_mod_kernel<8>, grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out);
+  else if (vec <= kMaxVec)
+    hipLaunchKernelGGL(ln_mod_kernel<kMaxVec>, grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out);
+  else
+    return fail(PKV_ERR_UNSUPPORTED, "dit_layer_norm: cols (%d) above %d", cols, 64 * 4 * kMaxVec);
+  return check_launch("ln_mod_kernel");
+}
+
+extern "C" int pkv_dit_rms_norm(const uint16_t *x, int64_t x_row_stride, int64_t rows, int32_t cols, const float *weight,
+                                float eps, uint16_t *out, int64_t out_row_stride, pkv_stream_t stream) {
+  if (rows == 0) return PKV_OK;
+  if (!x || !out || rows < 0 || cols <= 0) return fail(PKV_ERR_INVALID, "dit_rms_norm: bad arguments");
+  if (cols % 8 || x_row_stride % 8 || out_row_stride % 8 || x_row_stride < cols || out_row_stride < cols)
+    return fail(PKV_ERR_INVALID, "dit_rms_norm: cols and row strides must be multiples of 8 (cols %d)", cols);
+  if (rows > 0x7fffffffLL * kDitRowsPerBlock) return fail(PKV_ERR_UNSUPPORTED, "dit_rms_norm: too many rows");
+  const int vec = (cols / 8 + 63) / 64;
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(row_grid(rows)), block(64 * kDitRowsPerBlock);
+  if (vec <= 4)
+    hipLaunchKernelGGL(rms_kernel<4>, grid, block, 0, st, x, x_row_stride, rows, cols, weight, eps, out, out_row_stride);
+  else if (vec <= kMaxVec)
+    hipLaunchKernelGGL(rms_kernel<kMaxVec>, grid, block, 0, st, x, x_row_stride, rows, cols, weight, eps, out,
+                       out_row_stride);
+  else
+    return fail(PKV_ERR_UNSUPPORTED, "dit_rms_norm: cols (%d) above %d", cols, 64 * 8 * kMaxVec);
+  return check_launch("rms_kernel");
+}
+
+extern "C" int pkv_dit_residual(float *x, int64_t rows, int32_t cols, const uint16_t *y, int64_t y_row_stride,
+                                const float *gate, pkv_stream_t stream) {
+  if (rows == 0) return PKV_OK;
+  if (!x || !y || rows < 0 || cols <= 0) return fail(PKV_ERR_INVALID, "dit_residual: bad arguments");
+  if (cols % 4 || y_row_stride % 4 || y_row_stride < cols)
+    return fail(PKV_ERR_INVALID, "dit_residual: cols and the row stride must be multiples of 4 (cols %d)", cols);
+  hipLaunchKernelGGL(residual_kernel, dim3(flat_grid(rows * (cols / 4))), dim3(256), 0, as_stream(stream), x, rows,
+                     cols, y, y_row_stride, gate);
+  return check_launch("residual_kernel");
+}
+
+extern "C" int pkv_dit_gelu_tanh(const uint16_t *x, int64_t n, uint16_t *out, pkv_stream_t stream) {
+  if (n == 0) return PKV_OK;
+  if (!x || !out || n < 0) return fail(PKV_ERR_INVALID, "dit_gelu_tanh: bad arguments");
+  if (n % 8) return fail(PKV_ERR_INVALID, "dit_gelu_tanh: n (%lld) must be a multiple of 8", static_cast<long long>(n));
+  hipLaunchKernelGGL(gelu_tanh_kernel, dim3(flat_grid(n / 8)), dim3(256), 0, as_stream(stream), x, n / 8, out);
+  return check_launch("gelu_tanh_kernel");
+}

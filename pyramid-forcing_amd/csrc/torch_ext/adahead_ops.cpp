@@ -5,7 +5,8 @@
 // arguments like the reference, then calls the C ABI of
 // libpyramidkv_hip.so (include/pyramidkv_hip.h) with raw device pointers and
 // the current HIP stream.  Ops added by this build (ragged_attention,
-// rope_apply, cache_update, mega_merge_accum_weighted) are registered in
+// rope_apply, cache_update, mega_merge_accum_weighted and the dit_* row
+// operations of the end-to-end rollout's model) are registered in
 // the same namespace.
 
 #include <ATen/ATen.h>
@@ -601,6 +602,62 @@ static Tensor rope_apply(Tensor k, Tensor pos, Tensor ft, Tensor fy, Tensor fx) 
   return out;
 }
 
+// ---- DiT block row operations (the end-to-end rollout's model around the cache)
+static const float *f32_or_null(const c10::optional<Tensor> &t, int64_t n, const Tensor &like, const char *who) {
+  if (!t.has_value() || !t->defined()) return nullptr;
+  TORCH_CHECK(t->is_cuda() && t->device() == like.device() && t->scalar_type() == at::kFloat && t->is_contiguous() &&
+                  t->numel() == n,
+              who, ": vector arguments must be contiguous fp32 of the row length on the input's device");
+  return t->data_ptr<float>();
+}
+
+static Tensor dit_layer_norm(Tensor x, c10::optional<Tensor> mul, c10::optional<Tensor> add, bool mul_plus_one,
+                             double eps) {
+  TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat && x.dim() >= 1, "dit_layer_norm: x must be CUDA fp32");
+  auto xc = x.contiguous();
+  const int64_t C = xc.size(-1), rows = C ? xc.numel() / C : 0;
+  Tensor out = at::empty(xc.sizes(), xc.options().dtype(at::kBFloat16));
+  pkv_check(pkv_dit_layer_norm(xc.data_ptr<float>(), rows, static_cast<int32_t>(C), f32_or_null(mul, C, xc, "dit_layer_norm"),
+                               f32_or_null(add, C, xc, "dit_layer_norm"), mul_plus_one ? 1 : 0, static_cast<float>(eps),
+                               reinterpret_cast<uint16_t *>(out.data_ptr()), stream_for(xc)),
+            "dit_layer_norm");
+  return out;
+}
+
+static Tensor dit_rms_norm(Tensor x, c10::optional<Tensor> weight, double eps) {
+  TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kBFloat16 && x.dim() == 2 && x.stride(1) == 1,
+              "dit_rms_norm: x must be a CUDA bf16 [rows, cols] tensor with dense rows");
+  const int64_t rows = x.size(0), C = x.size(1);
+  Tensor out = at::empty({rows, C}, x.options());
+  pkv_check(pkv_dit_rms_norm(reinterpret_cast<const uint16_t *>(x.data_ptr()), x.stride(0), rows, static_cast<int32_t>(C),
+                             f32_or_null(weight, C, x, "dit_rms_norm"), static_cast<float>(eps),
+                             reinterpret_cast<uint16_t *>(out.data_ptr()), C, stream_for(x)),
+            "dit_rms_norm");
+  return out;
+}
+
+static void dit_residual_(Tensor x, Tensor y, c10::optional<Tensor> gate) {
+  TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat && x.dim() == 2 && x.is_contiguous(),
+              "dit_residual_: x must be a contiguous CUDA fp32 [rows, cols] tensor");
+  TORCH_CHECK(y.scalar_type() == at::kBFloat16 && y.dim() == 2 && y.sizes() == x.sizes() && y.stride(1) == 1 &&
+                  y.device() == x.device(),
+              "dit_residual_: y must be bf16 of x's shape with dense rows");
+  pkv_check(pkv_dit_residual(x.data_ptr<float>(), x.size(0), static_cast<int32_t>(x.size(1)),
+                             reinterpret_cast<const uint16_t *>(y.data_ptr()), y.stride(0),
+                             f32_or_null(gate, x.size(1), x, "dit_residual_"), stream_for(x)),
+            "dit_residual_");
+}
+
+static Tensor dit_gelu_tanh(Tensor x) {
+  TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kBFloat16, "dit_gelu_tanh: x must be CUDA bf16");
+  auto xc = x.contiguous();
+  Tensor out = at::empty_like(xc);
+  pkv_check(pkv_dit_gelu_tanh(reinterpret_cast<const uint16_t *>(xc.data_ptr()), xc.numel(),
+                              reinterpret_cast<uint16_t *>(out.data_ptr()), stream_for(xc)),
+            "dit_gelu_tanh");
+  return out;
+}
+
 // Fused MegaCache.update for one layer (see pkv_cache_update).
 static void cache_update(Mgr mgr, Tensor states_layer, Tensor sink_caps_layer, Tensor committed_vc_layer,
                          Tensor new_k, Tensor new_v, int64_t layer, int64_t t0, int64_t pass_kind,
@@ -907,6 +964,12 @@ static Tensor attn(Tensor q, Tensor, Tensor, Tensor, Tensor, int64_t, double, bo
   return at::empty_like(q);
 }
 static Tensor rope(Tensor k, Tensor, Tensor, Tensor, Tensor) { return at::empty_like(k); }
+static Tensor dit_ln(Tensor x, c10::optional<Tensor>, c10::optional<Tensor>, bool, double) {
+  return at::empty(x.sizes(), x.options().dtype(at::kBFloat16));
+}
+static Tensor dit_rms(Tensor x, c10::optional<Tensor>, double) { return at::empty({x.size(0), x.size(1)}, x.options()); }
+static void dit_residual(Tensor, Tensor, c10::optional<Tensor>) {}
+static Tensor dit_gelu(Tensor x) { return at::empty_like(x); }
 static void cache_update(Mgr, Tensor, Tensor, Tensor, Tensor, Tensor, int64_t, int64_t, int64_t, int64_t, int64_t,
                          bool) {}
 static void scatter_copy(Tensor, Tensor, Tensor, Tensor, int64_t) {}
@@ -1004,6 +1067,10 @@ TORCH_LIBRARY(adahead, m) {
         "int max_seqlen_q, float softmax_scale, bool kv_per_head=True, bool causal=False) -> Tensor");
   m.def("rope_apply(Tensor k, Tensor pos, Tensor freqs_ft_flat, Tensor freqs_fy_flat, Tensor freqs_fx_flat) "
         "-> Tensor");
+  m.def("dit_layer_norm(Tensor x, Tensor? mul, Tensor? add, bool mul_plus_one, float eps) -> Tensor");
+  m.def("dit_rms_norm(Tensor x, Tensor? weight, float eps) -> Tensor");
+  m.def("dit_residual_(Tensor(a!) x, Tensor y, Tensor? gate) -> ()");
+  m.def("dit_gelu_tanh(Tensor x) -> Tensor");
   m.def("cache_update(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, Tensor(a!) states_layer, "
         "Tensor sink_caps_layer, Tensor(b!) committed_vc_layer, Tensor new_k, Tensor new_v, int layer, int t0, "
         "int pass_kind, int shift_pending, int spatial_width, bool has_merge_head) -> ()");
@@ -1032,6 +1099,10 @@ TORCH_LIBRARY_IMPL(adahead, CUDA, m) {
   m.impl("mega_merge_accum_weighted", adahead::mega_merge_accum_weighted);
   m.impl("ragged_attention", adahead::ragged_attention);
   m.impl("rope_apply", adahead::rope_apply);
+  m.impl("dit_layer_norm", adahead::dit_layer_norm);
+  m.impl("dit_rms_norm", adahead::dit_rms_norm);
+  m.impl("dit_residual_", adahead::dit_residual_);
+  m.impl("dit_gelu_tanh", adahead::dit_gelu_tanh);
   m.impl("cache_update", adahead::cache_update);
   m.impl("scatter_copy", adahead::scatter_copy);
   m.impl("apply_pos_override", adahead::apply_pos_override);
@@ -1060,6 +1131,10 @@ TORCH_LIBRARY_IMPL(adahead, Meta, m) {
   m.impl("mega_plan_multi", adahead_meta::plan_multi);
   m.impl("ragged_attention", adahead_meta::attn);
   m.impl("rope_apply", adahead_meta::rope);
+  m.impl("dit_layer_norm", adahead_meta::dit_ln);
+  m.impl("dit_rms_norm", adahead_meta::dit_rms);
+  m.impl("dit_residual_", adahead_meta::dit_residual);
+  m.impl("dit_gelu_tanh", adahead_meta::dit_gelu);
   m.impl("cache_update", adahead_meta::cache_update);
   m.impl("scatter_copy", adahead_meta::scatter_copy);
   m.impl("apply_pos_override", adahead_meta::pos_override);

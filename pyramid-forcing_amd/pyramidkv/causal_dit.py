@@ -103,6 +103,9 @@ class CausalDiT:
                 "cnorm_q": torch.ones(s.dim, device=device), "cnorm_k": torch.ones(s.dim, device=device),
                 "ffn1": _linear(s.dim, s.ffn, g, device), "ffn2": _linear(s.ffn, s.dim, g, device),
             }
+            # q, k and v as one [3*dim, dim] GEMM
+            blk["qkv"] = (torch.cat([blk["q"][0], blk["k"][0], blk["v"][0]]).contiguous(),
+                          torch.cat([blk["q"][1], blk["k"][1], blk["v"][1]]).contiguous())
             self.blocks.append(blk)
         self.head_mod = torch.randn(2, s.dim, generator=g, device=device) / s.dim ** 0.5
         self.w_head = _linear(s.dim, self.patch_in, g, device)
@@ -117,11 +120,17 @@ class CausalDiT:
         return F.linear(x.to(torch.bfloat16), w, b)
 
     def _rms(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.s.eps) * weight).to(torch.bfloat16)
+        """WanRMSNorm on bf16 rows (a column slice of a wider GEMM output is
+        fine): bf16(x * rsqrt(mean(x^2) + eps) * weight), one HIP launch."""
+        return _ops.ops().dit_rms_norm(x, weight, self.s.eps)
 
-    def _ln(self, x: torch.Tensor, w=None, b=None) -> torch.Tensor:
-        return F.layer_norm(x.float(), (self.s.dim,), w, b, self.s.eps)
+    def _ln_mod(self, x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
+        """bf16(LN(x) * (1 + scale) + shift) of the fp32 residual stream."""
+        return _ops.ops().dit_layer_norm(x, scale, shift, True, self.s.eps)
+
+    def _ln_affine(self, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        """bf16(LN(x) * w + b), WanLayerNorm with elementwise affine."""
+        return _ops.ops().dit_layer_norm(x, w, b, False, self.s.eps)
 
     def _query_pos(self, t0: int, frames: int) -> torch.Tensor:
         """(t, y, x) of every (token, head) row of the roped query, t absolute."""
@@ -169,12 +178,15 @@ class CausalDiT:
         if not hasattr(self, "_cu_q") or self._cu_q_n != N:
             self._cu_q = torch.tensor([0, N], dtype=torch.int32, device=self.device)
             self._cu_q_n = N
+        ops = _ops.ops()
+        D = s.dim
         for bi, blk in enumerate(self.blocks):
             mod = blk["mod"] + e0
-            xn = self._ln(x) * (1 + mod[1]) + mod[0]
-            q = self._rms(self._mm(xn, blk["q"]), blk["norm_q"])
-            k = self._rms(self._mm(xn, blk["k"]), blk["norm_k"])
-            v = self._mm(xn, blk["v"])
+            xn = self._ln_mod(x, mod[1], mod[0])
+            qkv = self._mm(xn, blk["qkv"])
+            q = self._rms(qkv[:, :D], blk["norm_q"])
+            k = self._rms(qkv[:, D:2 * D], blk["norm_k"])
+            v = qkv[:, 2 * D:]
             q_rot = _ops.ops().rope_apply(q.view(N * s.heads, s.head_dim), qpos, *self.freq_parts_flat)
             if timer is not None:
                 timer(bi, "begin")
@@ -184,19 +196,19 @@ class CausalDiT:
             y = cache.attend(q_rot.view(1, N, s.heads, s.head_dim), current_start)
             if timer is not None:
                 timer(bi, "end")
-            x = x + self._mm(y.view(N, s.dim), blk["o"]).float() * mod[2]
+            ops.dit_residual_(x, self._mm(y.view(N, s.dim), blk["o"]), mod[2])
             # cross-attention to the cached text K/V
-            xc = self._ln(x, blk["norm3_w"], blk["norm3_b"])
+            xc = self._ln_affine(x, blk["norm3_w"], blk["norm3_b"])
             qc = self._rms(self._mm(xc, blk["cq"]), blk["cnorm_q"]).view(N, s.heads, s.head_dim)
             kc, vc = self.cross_kv[bi]
             yc = _ops.ragged_attention(qc, kc, vc, self._cu_q, self._cu_text, N, None, kv_per_head=False)
-            x = x + self._mm(yc.view(N, s.dim), blk["co"]).float()
+            ops.dit_residual_(x, self._mm(yc.view(N, s.dim), blk["co"]), None)
             # feed-forward
-            xn2 = self._ln(x) * (1 + mod[4]) + mod[3]
-            h = F.gelu(self._mm(xn2, blk["ffn1"]).float(), approximate="tanh")
-            x = x + self._mm(h, blk["ffn2"]).float() * mod[5]
+            xn2 = self._ln_mod(x, mod[4], mod[3])
+            h = ops.dit_gelu_tanh(self._mm(xn2, blk["ffn1"]))
+            ops.dit_residual_(x, self._mm(h, blk["ffn2"]), mod[5])
         hm = self.head_mod + e.view(1, s.dim)
-        out = self._mm(self._ln(x) * (1 + hm[1]) + hm[0], self.w_head)
+        out = self._mm(self._ln_mod(x, hm[1], hm[0]), self.w_head)
         return out.view(Fr, s.grid_h, s.grid_w, C, ph, pw).permute(3, 0, 1, 4, 2, 5).reshape(C, Fr, Hl, Wl)
 
 

@@ -66,3 +66,49 @@ def test_causal_dit_rollout_small():
     x = torch.randn(s.in_channels, 3, s.grid_h * 2, s.grid_w * 2, generator=g, device=DEV).to(torch.bfloat16)
     vel = model.forward(x, 500.0, 4 * 3 * s.frame_seqlen, caches, "noisy")
     assert vel.shape == x.shape and torch.isfinite(vel.float()).all()
+
+
+def _bf16_close(got: torch.Tensor, want: torch.Tensor, ulps: float = 1.0) -> None:
+    """got (bf16 result) within `ulps` bf16 units of the float64 value want
+    (a unit is 2^-7 of the value's binade; a small floor covers near-zeros)."""
+    g, w = got.double(), want.double()
+    tol = ulps * 2.0 ** -7 * w.abs() + 1e-6
+    bad = (g - w).abs() > tol
+    assert not bad.any(), (g[bad][:5], w[bad][:5])
+
+
+@pytest.mark.parametrize("rows,C", [(4680, 1536), (37, 256), (5, 4096)])
+def test_dit_row_ops_vs_float64(rows, C):
+    """The DiT block's row operations (LayerNorm with modulation or affine
+    weights, RMSNorm of a column slice, gated residual, tanh GELU) against
+    float64 torch formulas; bf16 results within one bf16 unit, the fp32
+    residual within fp32 rounding."""
+    import torch.nn.functional as F
+    from pyramidkv import _ops
+    ops = _ops.ops()
+    g = torch.Generator(device=DEV)
+    g.manual_seed(rows + C)
+    eps = 1e-6
+    x = torch.randn(rows, C, generator=g, device=DEV) * 3.0 + 1.5  # a mean well away from 0
+    scale = torch.randn(C, generator=g, device=DEV) * 0.1
+    shift = torch.randn(C, generator=g, device=DEV) * 0.1
+    ln = F.layer_norm(x.double(), (C,), eps=eps)
+    _bf16_close(ops.dit_layer_norm(x, scale, shift, True, eps), ln * (1 + scale.double()) + shift.double())
+    _bf16_close(ops.dit_layer_norm(x, scale, shift, False, eps), ln * scale.double() + shift.double(), ulps=1.0)
+    _bf16_close(ops.dit_layer_norm(x, None, None, True, eps), ln)
+    wide = (torch.randn(rows, 3 * C, generator=g, device=DEV) * 2.0).to(torch.bfloat16)
+    col = wide[:, C:2 * C]
+    w = torch.rand(C, generator=g, device=DEV) + 0.5
+    cd = col.double()
+    _bf16_close(ops.dit_rms_norm(col, w, eps), cd * torch.rsqrt(cd.pow(2).mean(-1, keepdim=True) + eps) * w.double())
+    x0 = torch.randn(rows, C, generator=g, device=DEV)
+    gate = torch.randn(C, generator=g, device=DEV)
+    xr = x0.clone()
+    ops.dit_residual_(xr, wide[:, :C], gate)
+    want = x0.double() + wide[:, :C].double() * gate.double()
+    assert ((xr.double() - want).abs() <= 2.0 ** -22 * (want.abs() + (wide[:, :C].double() * gate.double()).abs())).all()
+    xr = x0.clone()
+    ops.dit_residual_(xr, wide[:, :C], None)
+    assert torch.equal(xr, x0 + wide[:, :C].float())
+    hb = (torch.randn(rows, C, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
+    _bf16_close(ops.dit_gelu_tanh(hb), F.gelu(hb.double(), approximate="tanh"), ulps=1.0)
