@@ -41,139 +41,172 @@ struct PlanParams {
   int64_t sync_t[kMaxPlanChunks];
 };
 
-// Segment emission for one (chunk c, head h) by one wave, in the reference
-// order sink -> recent -> middle (Wave bucket of the current phase, or the
-// Anchor/lag ring in slot order) -> merge anchors (mega_plan.cc:133-264).
-// Every lane evaluates one candidate segment of that fixed order; a
+// Inclusive prefix sum over the 64 lanes of a wave by DPP: row shifts 1, 2,
+// 4, 8 scan each 16-lane row, then lane 15 of rows 0 and 2 is added to rows
+// 1 and 3 (row_bcast:15) and lane 31 to rows 2 and 3 (row_bcast:31).  Lanes
+// whose source lies outside the row (or rows the mask leaves out) add 0.
+__device__ inline int32_t wave_incl_sum(int32_t x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+
+// Per-(chunk, head) quantities shared by the pair's candidate segments.
+struct PairCtx {
+  int thresh, n_sink, n_recent, kind_s, b0, b1, tc, mcc;
+  int64_t sync_t;
+};
+
+__device__ inline PairCtx pair_ctx(const PlanParams &p, const HeadState &s, const int64_t *vc_h, int c) {
+  PairCtx x;
+  const int64_t t_c = p.t[c];
+  x.sync_t = p.sync_t[c];
+  x.thresh = s.sink_capacity;
+  const int n_sink_raw = static_cast<int>(vc_h[0]);
+  x.n_sink = (x.thresh > 0 && x.thresh < n_sink_raw) ? x.thresh : n_sink_raw;
+  x.n_recent = static_cast<int>(vc_h[2]);
+  x.kind_s = s.kind;
+  const int period = s.period > 0 ? s.period : 1;
+  const int bucket_cap = s.bucket_cap > 0 ? s.bucket_cap : 1;
+  // the reference's ((t % period) + period) % period; 32-bit when t fits
+  const int phase = (t_c >= 0 && t_c <= 0x7fffffff)
+                        ? static_cast<int>(static_cast<uint32_t>(t_c) % static_cast<uint32_t>(period))
+                        : static_cast<int>(((t_c % period) + period) % period);
+  x.b0 = phase * kMaxBucket;
+  x.b1 = x.b0 + (bucket_cap < kMaxBucket ? bucket_cap : kMaxBucket);
+  x.tc = s.tkey_count;
+  x.mcc = s.merge_completed_count;
+  return x;
+}
+
+// Candidate j of a pair in the reference's fixed order sink -> recent ->
+// middle (Wave bucket of the current phase, or the Anchor/lag ring in slot
+// order) -> merge anchors (mega_plan.cc:133-264).
+struct Cand {
+  bool valid;
+  int kind, sg, len;
+  int64_t traw, tremap;
+};
+
+__device__ inline Cand eval_cand(const PlanParams &p, const HeadState &s, const int32_t *mtc_h, const PairCtx &x,
+                                 int h, int j) {
+  const int32_t recent_min_t = 0x7fffffff;
+  const int c_sink = p.max_sink, c_rec = c_sink + p.max_recent, c_mid = c_rec + kMaxTKeyed,
+            n_cand = c_mid + kMaxMergeBlocks;
+  Cand d{false, PKV_SEG_INACTIVE, 0, 0, -1, -1};
+  if (j < c_sink) {
+    d.valid = j < x.n_sink;
+    d.kind = PKV_SEG_SINK;
+    d.sg = p.slot_off[0] + h * p.max_sink + j;
+    d.len = p.FSEQ;
+    d.traw = j;
+    d.tremap = x.sync_t;
+  } else if (j < c_rec) {
+    const int r = j - c_sink;
+    d.valid = r < x.n_recent;
+    d.kind = PKV_SEG_RECENT;
+    d.sg = p.slot_off[2] + h * p.max_recent + r;
+    d.len = p.FSEQ;
+  } else if (j < c_mid) {
+    const int i = j - c_rec;
+    d.kind = PKV_SEG_MIDDLE;
+    d.len = p.FSEQ;
+    if (x.kind_s == SK_CYCLIC) {
+      const int idx = x.b0 + i;
+      if (idx < x.b1 && idx < kMaxPhase * kMaxBucket) {
+        const int32_t t = s.cyclic_t[idx];
+        d.valid = s.cyclic_slot[idx] >= 0 && t >= x.thresh && t < recent_min_t;
+        d.sg = p.slot_off[1] + h * p.max_middle + idx;
+        d.traw = t;
+        d.tremap = x.sync_t;
+      }
+    } else if (x.kind_s == SK_STRIDE || x.kind_s == SK_LAG) {
+      if (i < x.tc) {
+        const int32_t t = s.tkey_t[i];
+        d.valid = t >= x.thresh && t < recent_min_t;
+        d.sg = p.slot_off[1] + h * p.max_middle + i;
+        d.traw = t;
+        d.tremap = x.kind_s == SK_STRIDE ? x.sync_t : -1;
+      }
+    }
+  } else if (j < n_cand) {
+    const int i = j - c_mid;
+    if (x.kind_s == SK_MERGE && i < x.mcc) {
+      const int slot = s.merge_completed_slot[i];
+      if (slot >= 0 && slot < p.MMB && s.merge_completed_start_t[i] > 0 && s.merge_completed_end_t[i] < recent_min_t) {
+        const int32_t tok = mtc_h[slot];
+        d.valid = tok > 0;
+        d.kind = PKV_SEG_MERGE;
+        d.sg = p.slot_off[3] + h * p.MMB + slot;
+        d.len = tok;
+        d.traw = 0;
+        d.tremap = s.merge_completed_median_t[i];
+      }
+    }
+  }
+  return d;
+}
+
+__device__ inline void put_seg(const pkv_plan_out &o, int i, const Cand &d, int32_t dst) {
+  o.src_kind[i] = d.kind;
+  o.src_slot_global[i] = d.sg;
+  o.seg_lengths[i] = d.len;
+  o.dst_token_offsets[i] = dst;
+  o.anchor_t_raw[i] = d.traw;
+  o.anchor_t_remap[i] = d.tremap;
+}
+
+__device__ inline void put_inactive(const pkv_plan_out &o, int i) {
+  put_seg(o, i, Cand{false, PKV_SEG_INACTIVE, 0, 0, -1, -1}, 0);
+}
+
+// Segment emission for one (chunk c, head h) by one wave (the general path,
+// for any number of candidates).  Every lane evaluates one candidate; a
 // candidate's position is the number of valid candidates before it (ballot
 // popcount), positions >= S are dropped (the reference stops appending at
 // S), and the destination offsets are a wave prefix sum of the lengths.
 // Returns the pair's token total (uniform over the wave).
-__device__ inline int32_t wave_incl_sum(int32_t x, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int32_t y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
-  return x;
-}
-
 template <bool kWrite>
 __device__ int32_t emit_pair(const PlanParams &p, const HeadState &s, const int64_t *vc_h, const int32_t *mtc_h,
                              int c, int h, int base, int32_t dst0, const pkv_plan_out &o) {
   const int lane = threadIdx.x & 63;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int S = p.S;
-  const int64_t t_c = p.t[c], sync_t = p.sync_t[c];
-  const int thresh = s.sink_capacity;
-  const int32_t recent_min_t = 0x7fffffff;
-  const int n_sink_raw = static_cast<int>(vc_h[0]);
-  const int n_sink = (thresh > 0 && thresh < n_sink_raw) ? thresh : n_sink_raw;
-  const int n_recent = static_cast<int>(vc_h[2]);
-  const int kind_s = s.kind;
-  const int period = s.period > 0 ? s.period : 1;
-  const int bucket_cap = s.bucket_cap > 0 ? s.bucket_cap : 1;
-  const int phase = static_cast<int>(((t_c % period) + period) % period);
-  const int b0 = phase * kMaxBucket;
-  const int b1 = b0 + (bucket_cap < kMaxBucket ? bucket_cap : kMaxBucket);
-  const int tc = s.tkey_count;
-  const int mcc = s.merge_completed_count;
-  const int c_sink = p.max_sink, c_rec = c_sink + p.max_recent, c_mid = c_rec + kMaxTKeyed,
-            n_cand = c_mid + kMaxMergeBlocks;
+  const PairCtx x = pair_ctx(p, s, vc_h, c);
+  const int n_cand = p.max_sink + p.max_recent + kMaxTKeyed + kMaxMergeBlocks;
   int fp = 0;
   int32_t run = 0;
   for (int j0 = 0; j0 < n_cand; j0 += 64) {
-    const int j = j0 + lane;
-    bool valid = false;
-    int kind = PKV_SEG_INACTIVE, sg = 0, len = 0;
-    int64_t traw = -1, tremap = -1;
-    if (j < c_sink) {
-      valid = j < n_sink;
-      kind = PKV_SEG_SINK;
-      sg = p.slot_off[0] + h * p.max_sink + j;
-      len = p.FSEQ;
-      traw = j;
-      tremap = sync_t;
-    } else if (j < c_rec) {
-      const int r = j - c_sink;
-      valid = r < n_recent;
-      kind = PKV_SEG_RECENT;
-      sg = p.slot_off[2] + h * p.max_recent + r;
-      len = p.FSEQ;
-    } else if (j < c_mid) {
-      const int i = j - c_rec;
-      kind = PKV_SEG_MIDDLE;
-      len = p.FSEQ;
-      if (kind_s == SK_CYCLIC) {
-        const int idx = b0 + i;
-        if (idx < b1 && idx < kMaxPhase * kMaxBucket) {
-          const int32_t t = s.cyclic_t[idx];
-          valid = s.cyclic_slot[idx] >= 0 && t >= thresh && t < recent_min_t;
-          sg = p.slot_off[1] + h * p.max_middle + idx;
-          traw = t;
-          tremap = sync_t;
-        }
-      } else if (kind_s == SK_STRIDE || kind_s == SK_LAG) {
-        if (i < tc) {
-          const int32_t t = s.tkey_t[i];
-          valid = t >= thresh && t < recent_min_t;
-          sg = p.slot_off[1] + h * p.max_middle + i;
-          traw = t;
-          tremap = kind_s == SK_STRIDE ? sync_t : -1;
-        }
-      }
-    } else if (j < n_cand) {
-      const int i = j - c_mid;
-      if (kind_s == SK_MERGE && i < mcc) {
-        const int slot = s.merge_completed_slot[i];
-        if (slot >= 0 && slot < p.MMB && s.merge_completed_start_t[i] > 0 &&
-            s.merge_completed_end_t[i] < recent_min_t) {
-          const int32_t tok = mtc_h[slot];
-          valid = tok > 0;
-          kind = PKV_SEG_MERGE;
-          sg = p.slot_off[3] + h * p.MMB + slot;
-          len = tok;
-          traw = 0;
-          tremap = s.merge_completed_median_t[i];
-        }
-      }
-    }
-    const uint64_t mask = __ballot(valid);
+    const Cand d = eval_cand(p, s, mtc_h, x, h, j0 + lane);
+    const uint64_t mask = __ballot(d.valid);
     const int pos = fp + __popcll(mask & below);
-    const bool emit = valid && pos < S;
-    const int32_t l = emit ? len : 0;
-    const int32_t incl = wave_incl_sum(l, lane);
-    if (kWrite && emit) {
-      const int i = base + pos;
-      o.src_kind[i] = kind;
-      o.src_slot_global[i] = sg;
-      o.seg_lengths[i] = len;
-      o.dst_token_offsets[i] = dst0 + run + incl - l;
-      o.anchor_t_raw[i] = traw;
-      o.anchor_t_remap[i] = tremap;
-    }
+    const bool emit = d.valid && pos < S;
+    const int32_t l = emit ? d.len : 0;
+    const int32_t incl = wave_incl_sum(l);
+    if (kWrite && emit) put_seg(o, base + pos, d, dst0 + run + incl - l);
     run += __shfl(incl, 63);
     fp = min(S, fp + __popcll(mask));
   }
   if (kWrite)
-    for (int i = fp + lane; i < S; i += 64) {
-      const int jj = base + i;
-      o.src_kind[jj] = PKV_SEG_INACTIVE;
-      o.src_slot_global[jj] = 0;
-      o.seg_lengths[jj] = 0;
-      o.dst_token_offsets[jj] = 0;
-      o.anchor_t_raw[jj] = -1;
-      o.anchor_t_remap[jj] = -1;
-    }
+    for (int i = fp + lane; i < S; i += 64) put_inactive(o, base + i);
   return run;
 }
 
 // One workgroup.  The layer's state records, counters and merge token counts
-// are staged in LDS with coalesced reads (when they fit), a count-only pass
-// gives every (chunk, head) pair its token total, a block-wide exclusive scan
-// turns those into offsets, and a second pass emits each pair's segments
-// with final destination offsets.
+// are staged in LDS with coalesced reads (when they fit).
+//  - One-pass form (at most 64 candidates and segments per pair, at most 64
+//    pairs): each wave evaluates the candidates of up to kPlanRegRounds pairs
+//    once and keeps them in registers; one barrier publishes the pair totals,
+//    every wave scans those 64 values itself and writes its segments.
+//  - General form: a count-only pass gives every pair its token total, a
+//    block-wide exclusive scan turns those into offsets, and a second pass
+//    re-evaluates each pair's segments and writes them.
 constexpr int kPlanStageHeads = 48;  // heads whose records are staged in LDS
+constexpr int kPlanRegRounds = 4;    // pairs per wave held in registers by the one-pass form
 
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const HeadState *states,
                                                             const int64_t *vc, const int32_t *mtc,
@@ -198,23 +231,68 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
   const HeadState *st = staged ? s_states : states;
   const int64_t *vcs = staged ? s_vc : vc;
   const int32_t *mts = staged ? s_mtc : mtc;
-  const int wave = tid >> 6, n_waves = blockDim.x >> 6;
+  const int wave = tid >> 6, n_waves = blockDim.x >> 6, lane = tid & 63;
+  const int n_cand = p.max_sink + p.max_recent + kMaxTKeyed + kMaxMergeBlocks;
+  if (n_cand <= 64 && p.S <= 64 && pairs <= 64 && pairs <= n_waves * kPlanRegRounds) {
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    Cand cd[kPlanRegRounds];
+    int pos[kPlanRegRounds], excl[kPlanRegRounds], nv[kPlanRegRounds];
+    bool emit[kPlanRegRounds];
+#pragma unroll
+    for (int r = 0; r < kPlanRegRounds; ++r) {
+      const int q = wave + r * n_waves;
+      emit[r] = false;
+      pos[r] = excl[r] = nv[r] = 0;
+      if (q < pairs) {  // uniform over the wave
+        const int c = q / p.H, h = q % p.H;
+        const PairCtx x = pair_ctx(p, st[h], vcs + h * 3, c);
+        cd[r] = eval_cand(p, st[h], mts + h * p.MMB, x, h, lane);
+        const uint64_t mask = __ballot(cd[r].valid);
+        pos[r] = __popcll(mask & below);
+        emit[r] = cd[r].valid && pos[r] < p.S;
+        const int32_t l = emit[r] ? cd[r].len : 0;
+        const int32_t incl = wave_incl_sum(l);
+        excl[r] = incl - l;
+        nv[r] = min(p.S, __popcll(mask));
+        if (lane == 63) len[q] = incl;
+      }
+    }
+    __syncthreads();
+    const int32_t v = lane < pairs ? len[lane] : 0;
+    const int32_t incl = wave_incl_sum(v);  // lane q: end offset of pair q
+    const int32_t total = __shfl(incl, 63);
+    if (tid == 0) {
+      o.cu_seqlens_k[0] = 0;
+      if (total_out) *total_out = total;
+    }
+#pragma unroll
+    for (int r = 0; r < kPlanRegRounds; ++r) {
+      const int q = wave + r * n_waves;
+      if (q >= pairs) continue;  // uniform over the wave
+      const int32_t end = __shfl(incl, q);
+      const int32_t base = __shfl(incl - v, q);
+      const int i0 = q * p.S;
+      if (emit[r]) put_seg(o, i0 + pos[r], cd[r], base + excl[r]);
+      if (lane >= nv[r] && lane < p.S) put_inactive(o, i0 + lane);
+      if (lane == 0) o.cu_seqlens_k[q + 1] = end;
+    }
+    return;
+  }
   for (int q = wave; q < pairs; q += n_waves) {
     const int c = q / p.H, h = q % p.H;
     const int32_t n = emit_pair<false>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, 0, o);
-    if ((tid & 63) == 0) len[q] = n;
+    if (lane == 0) len[q] = n;
   }
   __syncthreads();
   // exclusive scan of len[0..pairs) in 64-pair chunks: each wave scans its
   // chunks with lane shuffles, wave 0 scans the chunk totals, and every
   // element gets its chunk's base (two barriers)
   __shared__ int32_t ctot[kMaxPlanPairs / 64];
-  const int lane = tid & 63;
   const int n_chunks = (pairs + 63) / 64;
   for (int ch = wave; ch < n_chunks; ch += n_waves) {
     const int q = ch * 64 + lane;
     const int32_t v = q < pairs ? len[q] : 0;
-    const int32_t incl = wave_incl_sum(v, lane);
+    const int32_t incl = wave_incl_sum(v);
     if (q < pairs) len[q] = incl - v;
     if (lane == 63) ctot[ch] = incl;
   }
@@ -224,7 +302,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
     for (int c0 = 0; c0 < n_chunks; c0 += 64) {
       const int ch = c0 + lane;
       const int32_t v = ch < n_chunks ? ctot[ch] : 0;
-      const int32_t incl = wave_incl_sum(v, lane);
+      const int32_t incl = wave_incl_sum(v);
       if (ch < n_chunks) ctot[ch] = run + incl - v;
       run += __shfl(incl, 63);
     }
@@ -238,7 +316,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
     const int c = q / p.H, h = q % p.H;
     const int32_t b = len[q];
     const int32_t n = emit_pair<true>(p, st[h], vcs + h * 3, mts + h * p.MMB, c, h, q * p.S, b, o);
-    if ((tid & 63) == 0) o.cu_seqlens_k[q + 1] = b + n;
+    if (lane == 0) o.cu_seqlens_k[q + 1] = b + n;
   }
   if (tid == 0 && total_out) *total_out = part[0];
 }
