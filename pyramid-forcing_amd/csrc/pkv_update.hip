@@ -788,12 +788,15 @@ __global__ void __launch_bounds__(256) scatter_merge_prep_kernel(ScatterArgs sa,
 // and at the end.
 constexpr int kAccMembersLds = 4096;  // staged member ids per workgroup
 constexpr int kAccBatch = 8;          // member tokens loaded per batch
+constexpr int kAccPreFrames = 4;      // merge frames whose members one thread loads up front
 
+template <bool kPre>
 __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a) {
   __shared__ int32_t s_desc[kMaxMergeFrames][4];
   __shared__ int32_t s_ng[kMaxMergeFrames];
   __shared__ int32_t s_w[kMaxMergeFrames];  // regular grid width, 0: CSR lists
   __shared__ float s_wsum[kMaxMergeFrames];
+  __shared__ float s_wt[kMaxMergeFrames];  // frame weights (1 without weights)
   __shared__ int32_t s_gs[kMaxMergeFrames][kGroupsPerWg + 1];  // member-slice offsets (relative to s_off)
   __shared__ int32_t s_off[kMaxMergeFrames];
   __shared__ int32_t s_mem[kAccMembersLds];
@@ -816,6 +819,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
     s_ng[tid] = merge ? a.ws.ng[di] : 0;
     s_w[tid] = merge ? a.ws.width[di] : 0;
     s_wsum[tid] = merge ? a.ws.wsum[di] : 1.0f;
+    s_wt[tid] = a.weights ? a.weights[tid] : 1.0f;
   }
   __syncthreads();
   if (tid == 0) {
@@ -861,16 +865,64 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
     }
   }
   __syncthreads();
+  // kPre (calls of 2 to kAccPreFrames frames), every merge frame on the
+  // regular grid of 2 x 2 patches (the production Veil groups): each thread
+  // issues the member loads of all its frames at once, so the frames cost one
+  // memory round trip instead of one each.  The additions keep their order.
+  bool pre = kPre && patch == 2 && a.F <= kAccPreFrames;
+  for (int f = 0; f < a.F && pre; ++f) pre = !s_desc[f][0] || s_w[f] > 0;
 
   for (int it = tid; it < kGroupsPerWg * cpt; it += blockDim.x) {
     const int gl = it / cpt, c = (it % cpt) * 8;
     const int g = g0 + gl;
     if (g >= MTPA) break;
+    constexpr int kPreF = kPre ? kAccPreFrames : 1;
+    uint4 fk[kPreF][4], fv[kPreF][4];
+    if (pre) {
+#pragma unroll
+      for (int f = 0; f < kPreF; ++f) {
+        if (f >= a.F || !s_desc[f][0] || g >= s_ng[f]) continue;
+        const int W = s_w[f];
+        const int gcols = W / 2;
+        const int gbase = (g / gcols) * 2 * W + (g % gcols) * 2;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int64_t so = a.src.off(f, h, gbase + (m >> 1) * W + (m & 1)) + c;
+          fk[f][m] = ld16(a.src.k + so);
+          fv[f][m] = ld16(a.src.v + so);
+        }
+      }
+    }
     float ak[8], av[8];
     int cur = -1;  // slot whose accumulators are in registers
     int pos = 0;   // start of the current frame's staged members
-    for (int f = 0; f < a.F; ++f) {
-      if (!s_desc[f][0]) continue;
+    // one member token (K and V chunks) added to the accumulators
+    auto add_token = [&](const uint4 &k4, const uint4 &v4, float w) {
+      const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
+      const uint32_t vw[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float k0 = bf16_to_f32(static_cast<uint16_t>(kw[e] & 0xffff));
+        const float k1 = bf16_to_f32(static_cast<uint16_t>(kw[e] >> 16));
+        const float v0 = bf16_to_f32(static_cast<uint16_t>(vw[e] & 0xffff));
+        const float v1 = bf16_to_f32(static_cast<uint16_t>(vw[e] >> 16));
+        if (a.weights) {
+          ak[2 * e] = __fadd_rn(ak[2 * e], __fmul_rn(w, k0));
+          ak[2 * e + 1] = __fadd_rn(ak[2 * e + 1], __fmul_rn(w, k1));
+          av[2 * e] = __fadd_rn(av[2 * e], __fmul_rn(w, v0));
+          av[2 * e + 1] = __fadd_rn(av[2 * e + 1], __fmul_rn(w, v1));
+        } else {
+          ak[2 * e] += k0;
+          ak[2 * e + 1] += k1;
+          av[2 * e] += v0;
+          av[2 * e + 1] += v1;
+        }
+      }
+    };
+    // one merge frame: slot switch, new-block reset, member additions and
+    // the finalize write (inlined with a constant f in the prefetch loop)
+    auto frame = [&](int f) {
+      if (!s_desc[f][0]) return;
       const int slot = s_desc[f][1], is_new = s_desc[f][2], fin = s_desc[f][3];
       const int ng = s_ng[f];
       const int fpos = pos;
@@ -892,14 +944,18 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
       }
       if (is_new)
         for (int e = 0; e < 8; ++e) { ak[e] = 0.0f; av[e] = 0.0f; }
-      const float w = a.weights ? a.weights[f] : 1.0f;
+      const float w = s_wt[f];
       // members of group g: closed form on the regular grid of width W
       // (ascending: rows of the patch, then columns), else the staged or
       // snapshotted CSR slice
       const int W = s_w[f];
       const int gcols = W > 0 ? W / patch : 1;
       const int gbase = W > 0 ? (g / gcols) * patch * W + (g % gcols) * patch : 0;
-      if (g < ng) {
+      if (g < ng && pre) {
+        // the 2 x 2 patch's tokens, loaded above in ascending order
+#pragma unroll
+        for (int m = 0; m < 4; ++m) add_token(fk[f % kPreF][m], fv[f % kPreF][m], w);
+      } else if (g < ng) {
         const int m0 = W > 0 ? 0 : s_gs[f][gl], m1 = W > 0 ? patch * patch : s_gs[f][gl + 1];
         const int32_t *gmem = a.ws.members + static_cast<int64_t>(h * a.F + f) * a.FSEQ + s_off[f];
         for (int mb = m0; mb < m1; mb += kAccBatch) {
@@ -915,28 +971,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
               vv[b] = ld16(a.src.v + so);
             }
 #pragma unroll
-          for (int b = 0; b < kAccBatch; ++b) {
-            if (b >= n) continue;
-            const uint32_t kw[4] = {kk[b].x, kk[b].y, kk[b].z, kk[b].w};
-            const uint32_t vw[4] = {vv[b].x, vv[b].y, vv[b].z, vv[b].w};
-            for (int e = 0; e < 4; ++e) {
-              const float k0 = bf16_to_f32(static_cast<uint16_t>(kw[e] & 0xffff));
-              const float k1 = bf16_to_f32(static_cast<uint16_t>(kw[e] >> 16));
-              const float v0 = bf16_to_f32(static_cast<uint16_t>(vw[e] & 0xffff));
-              const float v1 = bf16_to_f32(static_cast<uint16_t>(vw[e] >> 16));
-              if (a.weights) {
-                ak[2 * e] = __fadd_rn(ak[2 * e], __fmul_rn(w, k0));
-                ak[2 * e + 1] = __fadd_rn(ak[2 * e + 1], __fmul_rn(w, k1));
-                av[2 * e] = __fadd_rn(av[2 * e], __fmul_rn(w, v0));
-                av[2 * e + 1] = __fadd_rn(av[2 * e + 1], __fmul_rn(w, v1));
-              } else {
-                ak[2 * e] += k0;
-                ak[2 * e + 1] += k1;
-                av[2 * e] += v0;
-                av[2 * e + 1] += v1;
-              }
-            }
-          }
+          for (int b = 0; b < kAccBatch; ++b)
+            if (b < n) add_token(kk[b], vv[b], w);
         }
       }
       if (fin >= 0 && fin < a.MMB && g < ng) {
@@ -957,6 +993,13 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
         st16(a.ml.merge_k + (hp * MTPA + g) * D + c, ok);
         st16(a.ml.merge_v + (hp * MTPA + g) * D + c, ov);
       }
+    };
+    if (pre) {
+#pragma unroll
+      for (int f = 0; f < kPreF; ++f)
+        if (f < a.F) frame(f);
+    } else {
+      for (int f = 0; f < a.F; ++f) frame(f);
     }
     if (cur >= 0) {
       const int64_t ho = static_cast<int64_t>(h) * a.MMA + cur;
@@ -992,7 +1035,12 @@ static int merge_prep_smem(const MergeArgs &ma, const void *kernel, size_t &smem
 
 static int launch_merge_accum(const MergeArgs &ma, hipStream_t st) {
   dim3 grid((ma.MTPA + kGroupsPerWg - 1) / kGroupsPerWg, ma.H);
-  hipLaunchKernelGGL(merge_accum_kernel, grid, dim3(kMergeThreads), 0, st, ma);
+  // the member prefetch pays where several frames would each cost a memory
+  // round trip; single-frame calls keep the smaller register footprint
+  if (ma.F >= 2 && ma.F <= kAccPreFrames)
+    hipLaunchKernelGGL(merge_accum_kernel<true>, grid, dim3(kMergeThreads), 0, st, ma);
+  else
+    hipLaunchKernelGGL(merge_accum_kernel<false>, grid, dim3(kMergeThreads), 0, st, ma);
   return check_launch("merge_accum_kernel");
 }
 
