@@ -414,6 +414,13 @@ __device__ inline uint4 rope_chunk_rows(uint4 raw, const PairTab (&tabs)[4], con
 }
 
 __device__ inline uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// Read of a workgroup-uniform value that no thread writes during the kernel,
+// through the constant address space: the compiler issues it as a scalar load.
+template <typename T>
+__device__ inline T ld_uniform(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)(p);
+}
 __device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
 // streaming store (non-temporal): the flat K/V of one layer call is larger
 // than the caches, so its lines are not kept
@@ -458,12 +465,16 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     for (int e = 0; e < 4; ++e) tabs[e] = pair_tab(threadIdx.x % cpt, e, a.rope);
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int seg = it / a.tiles_per_seg, tile = it % a.tiles_per_seg;
-    const int kind = a.kind[seg];
+    // every descriptor field is read before the first test, by scalar loads
+    // in one round trip (seg < n_seg, so all of them are in bounds; the
+    // descriptors do not change while the kernel runs)
+    const int kind = ld_uniform(a.kind + seg);
+    const int len = ld_uniform(a.len + seg);
+    const int64_t sg = ld_uniform(a.sg + seg);
+    const int64_t dst = ld_uniform(a.dst + seg);
+    const int64_t tr_seg = a.fuse ? ld_uniform(a.tremap + seg) : -1;
     if (kind < 0 || kind > 3) continue;
-    const int len = a.len[seg];
     if (len <= 0 || tile * kPackTok >= len) continue;
-    const int64_t sg = a.sg[seg];
-    const int64_t dst = a.dst[seg];
     const int stride = (kind == PKV_SEG_MERGE) ? a.MTPA : a.FSEQ;
     // a segment starts at its slot and may run on through the following
     // slots of the pool (the legacy plan's whole-pool segments), never past
@@ -476,7 +487,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     uint16_t *ok = a.k_out + dst * a.D;
     uint16_t *ov = a.v_out + dst * a.D;
     const bool rope = a.fuse && sp;  // uniform over the workgroup
-    const int64_t tr = rope ? a.tremap[seg] : -1;
+    const int64_t tr = rope ? tr_seg : -1;
     // segments up to tiles_per_seg tiles long (every frame or merge anchor)
     // take one pass; longer ones are walked tiles_per_seg tiles at a time
     for (int tok0 = tile * kPackTok; tok0 < len; tok0 += a.tiles_per_seg * kPackTok) {
