@@ -90,6 +90,15 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
          (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
+// Read of a workgroup-uniform value that no thread writes while the kernel
+// runs (written by an earlier launch), through the constant address space:
+// the compiler issues it as a scalar load, which keeps it out of the vector
+// registers and lets several such reads share one wait.
+template <typename T>
+__device__ inline T ld_uniform(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)(p);
+}
+
 // ---- error plumbing (host) --------------------------------------------------
 
 void set_error(const char *fmt, ...);

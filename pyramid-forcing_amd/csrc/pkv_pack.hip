@@ -415,12 +415,6 @@ __device__ inline uint4 rope_chunk_rows(uint4 raw, const PairTab (&tabs)[4], con
 
 __device__ inline uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// Read of a workgroup-uniform value that no thread writes during the kernel,
-// through the constant address space: the compiler issues it as a scalar load.
-template <typename T>
-__device__ inline T ld_uniform(const T *p) {
-  return *(const __attribute__((address_space(4))) T *)(p);
-}
 __device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
 // streaming store (non-temporal): the flat K/V of one layer call is larger
 // than the caches, so its lines are not kept
