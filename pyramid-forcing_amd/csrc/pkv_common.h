@@ -62,6 +62,7 @@ struct HeadState {
 };
 
 static_assert(sizeof(HeadState) == 600, "HeadState must be 600 bytes");
+static_assert(sizeof(HeadState) % 8 == 0, "records are copied as 8-byte words");
 static_assert(offsetof(HeadState, cyclic_cursor) == 240, "layout");
 static_assert(offsetof(HeadState, tkey_slot) == 248, "layout");
 static_assert(offsetof(HeadState, tkey_count) == 440, "layout");
@@ -97,6 +98,28 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
 template <typename T>
 __device__ inline T ld_uniform(const T *p) {
   return *(const __attribute__((address_space(4))) T *)(p);
+}
+
+// Copy of n 8-byte words from global memory into LDS by the whole workgroup:
+// each thread issues kBatch reads before its LDS writes, so a batch costs one
+// memory round trip.  The reads are unconditional (indices past the end read
+// the last word): guarded reads sit in separate blocks, and at their joins
+// the compiler waits for each read before issuing the next.
+template <int kBatch = 4>
+__device__ inline void stage_words(uint2 *lds, const uint2 *g, int n) {
+  for (int i0 = 0; i0 < n; i0 += kBatch * static_cast<int>(blockDim.x)) {
+    uint2 v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int i = i0 + static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x);
+      v[k] = g[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int i = i0 + static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x);
+      if (i < n) lds[i] = v[k];
+    }
+  }
 }
 
 // ---- error plumbing (host) --------------------------------------------------

@@ -220,12 +220,29 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
   const int pairs = p.C * p.H;
   const bool staged = p.H <= kPlanStageHeads && p.MMB <= kMaxMergeBlocks;
   if (staged) {
-    const int words = p.H * static_cast<int>(sizeof(HeadState)) / 4;
-    const int32_t *src = reinterpret_cast<const int32_t *>(states);
-    int32_t *dst = reinterpret_cast<int32_t *>(s_states);
-    for (int i = tid; i < words; i += blockDim.x) dst[i] = src[i];
-    for (int i = tid; i < p.H * 3; i += blockDim.x) s_vc[i] = vc[i];
-    for (int i = tid; i < p.H * p.MMB; i += blockDim.x) s_mtc[i] = mtc[i];
+    // every read is issued before the LDS writes (one memory round trip for
+    // up to 4 * kPlanThreads record words); the counters fit one per thread
+    static_assert(kPlanStageHeads * 3 <= kPlanThreads && kPlanStageHeads * kMaxMergeBlocks <= kPlanThreads &&
+                      kPlanStageHeads * sizeof(HeadState) / 8 <= 4 * kPlanThreads,
+                  "staging sizes");
+    const int nvc = p.H * 3, nmtc = p.H * p.MMB;
+    const int nw = p.H * static_cast<int>(sizeof(HeadState)) / 8;
+    const uint2 *g = reinterpret_cast<const uint2 *>(states);
+    uint2 *l = reinterpret_cast<uint2 *>(s_states);
+    // reads with clamped indices, unconditional except the merge counts
+    // (which may be empty), issued last: a wait the compiler places after a
+    // guarded read then delays no other read
+    uint2 w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = g[min(tid + k * kPlanThreads, nw - 1)];
+    const int64_t v = vc[min(tid, nvc - 1)];
+    int32_t m = 0;
+    if (nmtc > 0) m = mtc[min(tid, nmtc - 1)];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (tid + k * kPlanThreads < nw) l[tid + k * kPlanThreads] = w[k];
+    if (tid < nvc) s_vc[tid] = v;
+    if (tid < nmtc) s_mtc[tid] = m;
   }
   __syncthreads();
   const HeadState *st = staged ? s_states : states;

@@ -187,10 +187,10 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(HeadState *states,
   __shared__ __attribute__((aligned(16))) HeadState s_st[kRouteHeads];
   const int h0 = blockIdx.x * kRouteHeads;
   const int nh = min(kRouteHeads, H - h0);
-  const int words = nh * static_cast<int>(sizeof(HeadState)) / 4;
-  int32_t *g = reinterpret_cast<int32_t *>(states + h0);
-  int32_t *l = reinterpret_cast<int32_t *>(s_st);
-  for (int i = threadIdx.x; i < words; i += blockDim.x) l[i] = g[i];
+  const int words = nh * static_cast<int>(sizeof(HeadState)) / 8;
+  uint2 *g = reinterpret_cast<uint2 *>(states + h0);
+  uint2 *l = reinterpret_cast<uint2 *>(s_st);
+  stage_words(l, g, words);
   __syncthreads();
   if (static_cast<int>(threadIdx.x) < nh)
     route_head(s_st[threadIdx.x], h0 + threadIdx.x, F, t0, pass_kind, shift_pending, max_sink, max_recent, sink_caps,
