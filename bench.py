@@ -41,8 +41,8 @@ ATTN_KERNEL = "attn_fwd_kernel<128>"
 # WRITE_SIZE x 1.000); profiles/hbm_traffic_counters.md lists the runs.
 TRAFFIC_BYTES = {
     "attn_fwd_kernel<128>": 5673.03e6 + 431.31e6,   # config 2, one launch (30 x 12 sequences)
-    "pack_kernel": 302.34e6 + 296.94e6,             # config 3, one layer call (mean over 273 launches)
-    "merge_accum_kernel": 13.58e6 + 5.70e6,         # config 4, one eviction (mean over 200 launches)
+    "pack_kernel": 305.15e6 + 296.94e6,             # config 3, one layer call (mean over 273 launches)
+    "merge_accum_kernel": 13.57e6 + 5.70e6,         # config 4, one eviction (mean over 200 launches)
 }
 
 
