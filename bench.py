@@ -95,6 +95,18 @@ def bench_attention(steps: int, warmup: int, seed: int = 0):
                 q=q, k=k, v=v, out=out, cu_k=cu_k)
 
 
+def host_cpu() -> str:
+    """Model name of the host CPU (first /proc/cpuinfo entry), for the CPU baselines."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline_attention(r, budget_s: float = 15.0, max_seqs: int = 8):
     """The oracle's attention (numpy float32 BLAS) on a bounded sample of the
     same launch: whole (layer, head) sequences of the GPU's own inputs, the
@@ -133,7 +145,7 @@ def cpu_baseline_attention(r, budget_s: float = 15.0, max_seqs: int = 8):
     except Exception:
         cores = os.cpu_count() or 1
     mean_err = err_sum / max(err_n, 1)
-    base = dict(value=flops / secs / 1e12, unit="TFLOP/s", cores=int(cores), kind="port",
+    base = dict(value=flops / secs / 1e12, unit="TFLOP/s", cores=int(cores), kind="port", host_cpu=host_cpu(),
                 sample=f"{n} whole (layer, head) sequences of the timed launch (Q=4680, mean Lk="
                        f"{np.mean([lk[i] for i in order[:n]]):.0f}), numpy float32 softmax attention, {secs:.1f} s")
     parity = dict(sequences=n, max_abs=round(worst, 6), mean_abs=round(mean_err, 7), tolerance=[2e-2, 2e-3],
@@ -326,7 +338,7 @@ def cache_step_parity_and_cpu(r, budget_s: float = 10.0):
             ok = (tot == total and np.array_equal(pcu, got["cu"]) and np.array_equal(k, got["k"])
                   and np.array_equal(v, got["v"]) and np.array_equal(p, got["pos"]))
     bytes_one = total * (2 * ROW + 2 * ROW + 48)
-    return ok, dict(value=round(bytes_one * n / secs / 1e9, 3), unit="GB/s", cores=1, kind="port",
+    return ok, dict(value=round(bytes_one * n / secs / 1e9, 3), unit="GB/s", cores=1, kind="port", host_cpu=host_cpu(),
                     sample=f"layer 0 of the step-40 plan + pack ({total} packed tokens, RoPE fused) by the oracle's "
                            f"C restatement, {n} repetitions in {secs:.1f} s, single thread")
 
@@ -446,6 +458,7 @@ def bench_merge(steps: int, warmup: int, seed: int = 0):
               and np.array_equal(got["mpos"].numpy(), oacc["mpos"]) and np.array_equal(got["mtc"].numpy(), oacc["mtc"]))
     return dict(ms=float(np.median(ms)), bytes=bytes_step, parity=bool(parity), graph_same=bool(graph_same),
                 cpu=dict(value=round(bytes_step / cpu_s / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                         host_cpu=host_cpu(),
                          sample=f"the same 40 evictions (state update + weighted merge accumulate, 12 heads) by the "
                                 f"oracle's C restatement, {cpu_s:.2f} s, single thread"))
 
