@@ -154,7 +154,29 @@ __global__ void __launch_bounds__(256) residual_kernel(float *x, int64_t rows, i
   }
 }
 
-// out = bf16(0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3)))) in fp32, 8 values per thread
+// out = bf16(0.5 x (1 + tanh(u))), u = sqrt(2 / pi) (x + 0.044715 x^3), in fp32, 8 values per thread.
+// 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)), so the value is x / (1 + 2^(t)) with
+// t = -2 log2(e) u: one v_exp_f32 and one v_rcp_f32 (each within about 1 ulp
+// of fp32, far below the bf16 rounding of the result) instead of a library
+// tanh.  Large |u| give x (t -> -inf) or a signed zero (t -> +inf).
+__device__ inline float gelu_tanh_f32(float x) {
+  constexpr float kC1 = -2.0f * 1.4426950408889634f * 0.7978845608028654f;  // -2 log2(e) sqrt(2/pi)
+  constexpr float kC3 = kC1 * 0.044715f;
+  const float t = x * fmaf(kC3, x * x, kC1);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+}
+
+// f32 pair -> bf16x2 by the hardware round-to-nearest-even conversion (NaN
+// halves to 0x7fc0, as pack_bf16x2)
+__device__ inline uint32_t cvt_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7fffu) > 0x7f80u) u = (u & 0xffff0000u) | 0x7fc0u;
+  if ((u & 0x7fff0000u) > 0x7f800000u) u = (u & 0xffffu) | 0x7fc00000u;
+  return u;
+}
+
 __global__ void __launch_bounds__(256) gelu_tanh_kernel(const uint16_t *x, int64_t n8, uint16_t *out) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n8;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -164,12 +186,7 @@ __global__ void __launch_bounds__(256) gelu_tanh_kernel(const uint16_t *x, int64
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float f[2] = {bf16_to_f32(static_cast<uint16_t>(wd[e] & 0xffff)), bf16_to_f32(static_cast<uint16_t>(wd[e] >> 16))};
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const float u = f[q];
-        f[q] = 0.5f * u * (1.0f + tanhf(0.7978845608028654f * (u + 0.044715f * u * u * u)));
-      }
-      o[e] = pack_bf16x2(f[0], f[1]);
+      o[e] = cvt_bf16x2(gelu_tanh_f32(f[0]), gelu_tanh_f32(f[1]));
     }
     *reinterpret_cast<uint4 *>(out + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
   }
