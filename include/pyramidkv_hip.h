@@ -351,6 +351,10 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools,
  *   NULL), in place; x fp32 [rows, cols], y bf16 with a row stride.
  * pkv_dit_gelu_tanh: out = bf16(gelu_tanh(float(x))) elementwise, n a
  *   multiple of 8.
+ * pkv_dit_residual_layer_norm: pkv_dit_residual, then pkv_dit_layer_norm of
+ *   the updated rows, in one pass over x (the residual update followed by
+ *   the next norm of causal_model.py:395-420); same results as the two
+ *   calls in sequence.
  */
 int pkv_dit_layer_norm(const float *x, int64_t rows, int32_t cols, const float *mul,
                        const float *add, int32_t mul_plus_one, float eps, uint16_t *out,
@@ -361,6 +365,10 @@ int pkv_dit_rms_norm(const uint16_t *x, int64_t x_row_stride, int64_t rows, int3
 int pkv_dit_residual(float *x, int64_t rows, int32_t cols, const uint16_t *y,
                      int64_t y_row_stride, const float *gate, pkv_stream_t stream);
 int pkv_dit_gelu_tanh(const uint16_t *x, int64_t n, uint16_t *out, pkv_stream_t stream);
+int pkv_dit_residual_layer_norm(float *x, int64_t rows, int32_t cols, const uint16_t *y,
+                                int64_t y_row_stride, const float *gate, const float *mul,
+                                const float *add, int32_t mul_plus_one, float eps, uint16_t *out,
+                                pkv_stream_t stream);
 
 #ifdef __cplusplus
 }

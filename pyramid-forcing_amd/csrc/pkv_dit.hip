@@ -27,16 +27,34 @@ __device__ inline float wave_sum(float x) {
 
 __device__ inline float4 ld_f4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
+// a + float(b) * gate[4j..4j+3] with one rounding per element (fma), or
+// a + float(b) without a gate: the residual update of 4 columns, shared by
+// the residual kernel and the fused residual + LayerNorm so both round alike
+__device__ inline float4 residual4(float4 a, uint2 b, const float *gate, int j) {
+  const float y0 = bf16_to_f32(static_cast<uint16_t>(b.x & 0xffff)), y1 = bf16_to_f32(static_cast<uint16_t>(b.x >> 16));
+  const float y2 = bf16_to_f32(static_cast<uint16_t>(b.y & 0xffff)), y3 = bf16_to_f32(static_cast<uint16_t>(b.y >> 16));
+  if (gate) {
+    const float4 g = ld_f4(gate + 4 * j);
+    return make_float4(__fmaf_rn(y0, g.x, a.x), __fmaf_rn(y1, g.y, a.y), __fmaf_rn(y2, g.z, a.z),
+                       __fmaf_rn(y3, g.w, a.w));
+  }
+  return make_float4(__fadd_rn(a.x, y0), __fadd_rn(a.y, y1), __fadd_rn(a.z, y2), __fadd_rn(a.w, y3));
+}
+
 // out[r, :] = bf16(LN(x[r, :]) * m + a), LN without affine weights; m =
-// (one_plus ? 1 + mul : mul) and a = add, each optional (1 and 0)
-template <int K>
-__global__ void __launch_bounds__(64 * kDitRowsPerBlock) ln_mod_kernel(const float *x, int64_t rows, int C,
+// (one_plus ? 1 + mul : mul) and a = add, each optional (1 and 0).  kRes
+// first applies the residual update x[r, :] += float(y[r, :]) * gate in
+// registers and writes the updated row back, so the row is read once.
+template <int K, bool kRes>
+__global__ void __launch_bounds__(64 * kDitRowsPerBlock) ln_mod_kernel(float *x, int64_t rows, int C,
                                                                        const float *mul, const float *add,
-                                                                       int one_plus, float eps, uint16_t *out) {
+                                                                       int one_plus, float eps, uint16_t *out,
+                                                                       const uint16_t *y, int64_t y_stride,
+                                                                       const float *gate) {
   const int lane = threadIdx.x & 63;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * kDitRowsPerBlock + (threadIdx.x >> 6);
   if (r >= rows) return;
-  const float *xr = x + r * C;
+  float *xr = x + r * C;
   const int nv = C / 4;
   float4 v[K];
   float s = 0.0f;
@@ -44,6 +62,10 @@ __global__ void __launch_bounds__(64 * kDitRowsPerBlock) ln_mod_kernel(const flo
   for (int k = 0; k < K; ++k) {
     const int j = lane + 64 * k;
     v[k] = j < nv ? ld_f4(xr + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (kRes && j < nv) {
+      v[k] = residual4(v[k], *reinterpret_cast<const uint2 *>(y + r * y_stride + 4 * j), gate, j);
+      *reinterpret_cast<float4 *>(xr + 4 * j) = v[k];
+    }
     s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
   }
   const float mean = wave_sum(s) / static_cast<float>(C);
@@ -135,22 +157,9 @@ __global__ void __launch_bounds__(256) residual_kernel(float *x, int64_t rows, i
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t r = i / nv;
     const int j = static_cast<int>(i % nv);
-    float4 a = ld_f4(x + r * C + 4 * j);
+    const float4 a = ld_f4(x + r * C + 4 * j);
     const uint2 b = *reinterpret_cast<const uint2 *>(y + r * y_stride + 4 * j);
-    float yv[4] = {bf16_to_f32(static_cast<uint16_t>(b.x & 0xffff)), bf16_to_f32(static_cast<uint16_t>(b.x >> 16)),
-                   bf16_to_f32(static_cast<uint16_t>(b.y & 0xffff)), bf16_to_f32(static_cast<uint16_t>(b.y >> 16))};
-    if (gate) {
-      const float4 g = ld_f4(gate + 4 * j);
-      yv[0] *= g.x;
-      yv[1] *= g.y;
-      yv[2] *= g.z;
-      yv[3] *= g.w;
-    }
-    a.x += yv[0];
-    a.y += yv[1];
-    a.z += yv[2];
-    a.w += yv[3];
-    *reinterpret_cast<float4 *>(x + r * C + 4 * j) = a;
+    *reinterpret_cast<float4 *>(x + r * C + 4 * j) = residual4(a, b, gate, j);
   }
 }
 
@@ -192,6 +201,36 @@ __global__ void __launch_bounds__(256) gelu_tanh_kernel(const uint16_t *x, int64
   }
 }
 
+static int row_grid(int64_t rows);
+
+// LayerNorm rows (kRes: after the residual update from y and gate)
+template <bool kRes>
+static int launch_ln_k(float *x, int64_t rows, int cols, const float *mul, const float *add, int mul_plus_one,
+                       float eps, uint16_t *out, const uint16_t *y, int64_t y_stride, const float *gate, hipStream_t st,
+                       const char *who) {
+  const int vec = (cols / 4 + 63) / 64;
+  const dim3 grid(row_grid(rows)), block(64 * kDitRowsPerBlock);
+  if (vec <= 4)
+    hipLaunchKernelGGL((ln_mod_kernel<4, kRes>), grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out, y,
+                       y_stride, gate);
+  else if (vec <= 8)
+    hipLaunchKernelGGL((ln_mod_kernel<8, kRes>), grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out, y,
+                       y_stride, gate);
+  else if (vec <= kMaxVec)
+    hipLaunchKernelGGL((ln_mod_kernel<kMaxVec, kRes>), grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps,
+                       out, y, y_stride, gate);
+  else
+    return fail(PKV_ERR_UNSUPPORTED, "%s: cols (%d) above %d", who, cols, 64 * 4 * kMaxVec);
+  return check_launch("ln_mod_kernel");
+}
+
+static int launch_ln(float *x, int64_t rows, int cols, const float *mul, const float *add, int mul_plus_one, float eps,
+                     uint16_t *out, const uint16_t *y, int64_t y_stride, const float *gate, hipStream_t st,
+                     const char *who) {
+  return y ? launch_ln_k<true>(x, rows, cols, mul, add, mul_plus_one, eps, out, y, y_stride, gate, st, who)
+           : launch_ln_k<false>(x, rows, cols, mul, add, mul_plus_one, eps, out, y, y_stride, gate, st, who);
+}
+
 static int row_grid(int64_t rows) {
   const int64_t g = (rows + kDitRowsPerBlock - 1) / kDitRowsPerBlock;
   return static_cast<int>(g);
@@ -213,18 +252,23 @@ extern "C" int pkv_dit_layer_norm(const float *x, int64_t rows, int32_t cols, co
   if (!x || !out || rows < 0 || cols <= 0) return fail(PKV_ERR_INVALID, "dit_layer_norm: bad arguments");
   if (cols % 4) return fail(PKV_ERR_INVALID, "dit_layer_norm: cols (%d) must be a multiple of 4", cols);
   if (rows > 0x7fffffffLL * kDitRowsPerBlock) return fail(PKV_ERR_UNSUPPORTED, "dit_layer_norm: too many rows");
-  const int vec = (cols / 4 + 63) / 64;
-  hipStream_t st = as_stream(stream);
-  const dim3 grid(row_grid(rows)), block(64 * kDitRowsPerBlock);
-  if (vec <= 4)
-    hipLaunchKernelGGL(ln_mod_kernel<4>, grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out);
-  else if (vec <= 8)
-    hipLaunchKernelGGL(ln_mod_kernel<8>, grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out);
-  else if (vec <= kMaxVec)
-    hipLaunchKernelGGL(ln_mod_kernel<kMaxVec>, grid, block, 0, st, x, rows, cols, mul, add, mul_plus_one, eps, out);
-  else
-    return fail(PKV_ERR_UNSUPPORTED, "dit_layer_norm: cols (%d) above %d", cols, 64 * 4 * kMaxVec);
-  return check_launch("ln_mod_kernel");
+  return launch_ln(const_cast<float *>(x), rows, cols, mul, add, mul_plus_one, eps, out, nullptr, 0, nullptr,
+                   as_stream(stream), "dit_layer_norm");
+}
+
+extern "C" int pkv_dit_residual_layer_norm(float *x, int64_t rows, int32_t cols, const uint16_t *y,
+                                           int64_t y_row_stride, const float *gate, const float *mul,
+                                           const float *add, int32_t mul_plus_one, float eps, uint16_t *out,
+                                           pkv_stream_t stream) {
+  if (rows == 0) return PKV_OK;
+  if (!x || !y || !out || rows < 0 || cols <= 0) return fail(PKV_ERR_INVALID, "dit_residual_layer_norm: bad arguments");
+  if (cols % 4 || y_row_stride % 4 || y_row_stride < cols)
+    return fail(PKV_ERR_INVALID, "dit_residual_layer_norm: cols and the row stride must be multiples of 4 (cols %d)",
+                cols);
+  if (rows > 0x7fffffffLL * kDitRowsPerBlock)
+    return fail(PKV_ERR_UNSUPPORTED, "dit_residual_layer_norm: too many rows");
+  return launch_ln(x, rows, cols, mul, add, mul_plus_one, eps, out, y, y_row_stride, gate, as_stream(stream),
+                   "dit_residual_layer_norm");
 }
 
 extern "C" int pkv_dit_rms_norm(const uint16_t *x, int64_t x_row_stride, int64_t rows, int32_t cols, const float *weight,

@@ -648,6 +648,26 @@ static void dit_residual_(Tensor x, Tensor y, c10::optional<Tensor> gate) {
             "dit_residual_");
 }
 
+static Tensor dit_residual_layer_norm_(Tensor x, Tensor y, c10::optional<Tensor> gate, c10::optional<Tensor> mul,
+                                       c10::optional<Tensor> add, bool mul_plus_one, double eps) {
+  TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat && x.dim() == 2 && x.is_contiguous(),
+              "dit_residual_layer_norm_: x must be a contiguous CUDA fp32 [rows, cols] tensor");
+  TORCH_CHECK(y.scalar_type() == at::kBFloat16 && y.dim() == 2 && y.sizes() == x.sizes() && y.stride(1) == 1 &&
+                  y.device() == x.device(),
+              "dit_residual_layer_norm_: y must be bf16 of x's shape with dense rows");
+  const int64_t C = x.size(1);
+  Tensor out = at::empty(x.sizes(), x.options().dtype(at::kBFloat16));
+  pkv_check(pkv_dit_residual_layer_norm(x.data_ptr<float>(), x.size(0), static_cast<int32_t>(C),
+                                        reinterpret_cast<const uint16_t *>(y.data_ptr()), y.stride(0),
+                                        f32_or_null(gate, C, x, "dit_residual_layer_norm_"),
+                                        f32_or_null(mul, C, x, "dit_residual_layer_norm_"),
+                                        f32_or_null(add, C, x, "dit_residual_layer_norm_"), mul_plus_one ? 1 : 0,
+                                        static_cast<float>(eps), reinterpret_cast<uint16_t *>(out.data_ptr()),
+                                        stream_for(x)),
+            "dit_residual_layer_norm_");
+  return out;
+}
+
 static Tensor dit_gelu_tanh(Tensor x) {
   TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kBFloat16, "dit_gelu_tanh: x must be CUDA bf16");
   auto xc = x.contiguous();
@@ -970,6 +990,10 @@ static Tensor dit_ln(Tensor x, c10::optional<Tensor>, c10::optional<Tensor>, boo
 static Tensor dit_rms(Tensor x, c10::optional<Tensor>, double) { return at::empty({x.size(0), x.size(1)}, x.options()); }
 static void dit_residual(Tensor, Tensor, c10::optional<Tensor>) {}
 static Tensor dit_gelu(Tensor x) { return at::empty_like(x); }
+static Tensor dit_res_ln(Tensor x, Tensor, c10::optional<Tensor>, c10::optional<Tensor>, c10::optional<Tensor>, bool,
+                         double) {
+  return at::empty(x.sizes(), x.options().dtype(at::kBFloat16));
+}
 static void cache_update(Mgr, Tensor, Tensor, Tensor, Tensor, Tensor, int64_t, int64_t, int64_t, int64_t, int64_t,
                          bool) {}
 static void scatter_copy(Tensor, Tensor, Tensor, Tensor, int64_t) {}
@@ -1071,6 +1095,8 @@ TORCH_LIBRARY(adahead, m) {
   m.def("dit_rms_norm(Tensor x, Tensor? weight, float eps) -> Tensor");
   m.def("dit_residual_(Tensor(a!) x, Tensor y, Tensor? gate) -> ()");
   m.def("dit_gelu_tanh(Tensor x) -> Tensor");
+  m.def("dit_residual_layer_norm_(Tensor(a!) x, Tensor y, Tensor? gate, Tensor? mul, Tensor? add, bool mul_plus_one, "
+        "float eps) -> Tensor");
   m.def("cache_update(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, Tensor(a!) states_layer, "
         "Tensor sink_caps_layer, Tensor(b!) committed_vc_layer, Tensor new_k, Tensor new_v, int layer, int t0, "
         "int pass_kind, int shift_pending, int spatial_width, bool has_merge_head) -> ()");
@@ -1103,6 +1129,7 @@ TORCH_LIBRARY_IMPL(adahead, CUDA, m) {
   m.impl("dit_rms_norm", adahead::dit_rms_norm);
   m.impl("dit_residual_", adahead::dit_residual_);
   m.impl("dit_gelu_tanh", adahead::dit_gelu_tanh);
+  m.impl("dit_residual_layer_norm_", adahead::dit_residual_layer_norm_);
   m.impl("cache_update", adahead::cache_update);
   m.impl("scatter_copy", adahead::scatter_copy);
   m.impl("apply_pos_override", adahead::apply_pos_override);
@@ -1135,6 +1162,7 @@ TORCH_LIBRARY_IMPL(adahead, Meta, m) {
   m.impl("dit_rms_norm", adahead_meta::dit_rms);
   m.impl("dit_residual_", adahead_meta::dit_residual);
   m.impl("dit_gelu_tanh", adahead_meta::dit_gelu);
+  m.impl("dit_residual_layer_norm_", adahead_meta::dit_res_ln);
   m.impl("cache_update", adahead_meta::cache_update);
   m.impl("scatter_copy", adahead_meta::scatter_copy);
   m.impl("apply_pos_override", adahead_meta::pos_override);

@@ -180,9 +180,16 @@ class CausalDiT:
             self._cu_q_n = N
         ops = _ops.ops()
         D = s.dim
+        eps = s.eps
+        mods = [blk["mod"] + e0 for blk in self.blocks]
+        hm = self.head_mod + e.view(1, s.dim)
+        # each residual update is fused with the norm that reads the updated
+        # stream next (one pass over x): attention -> cross-attention norm,
+        # cross-attention -> feed-forward norm, feed-forward -> the next
+        # block's (or the head's) modulated norm
+        xn = self._ln_mod(x, mods[0][1], mods[0][0])
         for bi, blk in enumerate(self.blocks):
-            mod = blk["mod"] + e0
-            xn = self._ln_mod(x, mod[1], mod[0])
+            mod = mods[bi]
             qkv = self._mm(xn, blk["qkv"])
             q = self._rms(qkv[:, :D], blk["norm_q"])
             k = self._rms(qkv[:, D:2 * D], blk["norm_k"])
@@ -196,19 +203,19 @@ class CausalDiT:
             y = cache.attend(q_rot.view(1, N, s.heads, s.head_dim), current_start)
             if timer is not None:
                 timer(bi, "end")
-            ops.dit_residual_(x, self._mm(y.view(N, s.dim), blk["o"]), mod[2])
             # cross-attention to the cached text K/V
-            xc = self._ln_affine(x, blk["norm3_w"], blk["norm3_b"])
+            xc = ops.dit_residual_layer_norm_(x, self._mm(y.view(N, s.dim), blk["o"]), mod[2], blk["norm3_w"],
+                                              blk["norm3_b"], False, eps)
             qc = self._rms(self._mm(xc, blk["cq"]), blk["cnorm_q"]).view(N, s.heads, s.head_dim)
             kc, vc = self.cross_kv[bi]
             yc = _ops.ragged_attention(qc, kc, vc, self._cu_q, self._cu_text, N, None, kv_per_head=False)
-            ops.dit_residual_(x, self._mm(yc.view(N, s.dim), blk["co"]), None)
             # feed-forward
-            xn2 = self._ln_mod(x, mod[4], mod[3])
+            xn2 = ops.dit_residual_layer_norm_(x, self._mm(yc.view(N, s.dim), blk["co"]), None, mod[4], mod[3], True,
+                                               eps)
             h = ops.dit_gelu_tanh(self._mm(xn2, blk["ffn1"]))
-            ops.dit_residual_(x, self._mm(h, blk["ffn2"]), mod[5])
-        hm = self.head_mod + e.view(1, s.dim)
-        out = self._mm(self._ln_mod(x, hm[1], hm[0]), self.w_head)
+            nxt = mods[bi + 1] if bi + 1 < len(self.blocks) else hm
+            xn = ops.dit_residual_layer_norm_(x, self._mm(h, blk["ffn2"]), mod[5], nxt[1], nxt[0], True, eps)
+        out = self._mm(xn, self.w_head)
         return out.view(Fr, s.grid_h, s.grid_w, C, ph, pw).permute(3, 0, 1, 4, 2, 5).reshape(C, Fr, Hl, Wl)
 
 

@@ -112,3 +112,29 @@ def test_dit_row_ops_vs_float64(rows, C):
     assert torch.equal(xr, x0 + wide[:, :C].float())
     hb = (torch.randn(rows, C, generator=g, device=DEV) * 3.0).to(torch.bfloat16)
     _bf16_close(ops.dit_gelu_tanh(hb), F.gelu(hb.double(), approximate="tanh"), ulps=1.0)
+
+
+@pytest.mark.parametrize("rows,C", [(4680, 1536), (37, 256), (5, 4096)])
+@pytest.mark.parametrize("gated,one_plus", [(True, True), (False, True), (True, False)])
+def test_dit_residual_layer_norm_equals_the_two_ops(rows, C, gated, one_plus):
+    """The fused residual update + LayerNorm leaves the same fp32 stream and
+    the same bf16 output as dit_residual_ followed by dit_layer_norm (bit
+    for bit), for gated and ungated updates and both scale forms."""
+    from pyramidkv import _ops
+    ops = _ops.ops()
+    g = torch.Generator(device=DEV)
+    g.manual_seed(7 * rows + C)
+    eps = 1e-6
+    x0 = torch.randn(rows, C, generator=g, device=DEV) * 2.0 + 0.5
+    wide = (torch.randn(rows, 2 * C, generator=g, device=DEV) * 2.0).to(torch.bfloat16)
+    y = wide[:, C:]  # a column slice: rows with a stride
+    gate = torch.randn(C, generator=g, device=DEV) if gated else None
+    mul = torch.randn(C, generator=g, device=DEV) * 0.1
+    add = torch.randn(C, generator=g, device=DEV) * 0.1
+    xa = x0.clone()
+    ops.dit_residual_(xa, y, gate)
+    want = ops.dit_layer_norm(xa, mul, add, one_plus, eps)
+    xb = x0.clone()
+    got = ops.dit_residual_layer_norm_(xb, y, gate, mul, add, one_plus, eps)
+    assert torch.equal(xb, xa)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
