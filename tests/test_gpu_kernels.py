@@ -330,3 +330,13 @@ def test_attention_rejects_causal_and_bad_head_dim():
     assert A.lib().pkv_ragged_attn_fwd(ctypes.byref(a), stream()) == A.PKV_ERR_UNSUPPORTED
     a.causal, a.head_dim = 0, 96
     assert A.lib().pkv_ragged_attn_fwd(ctypes.byref(a), stream()) == A.PKV_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("F,weighted", [(2, False), (4, False), (4, True)])
+def test_merge_multi_frame_calls_bit_exact(F, weighted):
+    # calls of 2 and 4 frames on the production grid (the accumulation's
+    # path that loads every frame's members at once), offset so that calls
+    # straddle block boundaries: one call finalizes a block and starts the
+    # next, in the same or the other slot
+    blocks = [[2 + F * b + f for f in range(F)] for b in range(24 // F)]
+    _merge_run(H=2, FSEQ=1560, W=52, blocks_t=blocks, seed=10 + F, weights=True if weighted else None)
