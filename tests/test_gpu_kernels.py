@@ -78,6 +78,31 @@ def test_plan_bit_exact(seed):
         assert int(total.item()) == want[7]
 
 
+@pytest.mark.parametrize("H,t_list", [(12, [60, 61, 62, 63, 64, 65]), (48, [90, 91])])
+def test_plan_bit_exact_beyond_64_pairs(H, t_list):
+    """More than 64 (chunk, head) pairs take the plan's two-pass form (count,
+    block-wide scan, emit) instead of the one-pass register form."""
+    rng = np.random.default_rng(H + len(t_list))
+    g = _geom(num_heads=H, max_attend_chunks=len(t_list))
+    dp = DevicePools(g)
+    host = O.states_to_bytes(_rand_states(rng, H))
+    for blk in range(30):
+        O.state_update(host, [3 * blk, 3 * blk + 1, 3 * blk + 2], 1)
+    vc = np.stack([rng.integers(0, 5, H), np.zeros(H, np.int64), rng.integers(0, 6, H)], 1).astype(np.int64)
+    mtc = rng.integers(0, 420, (H, 6)).astype(np.int32)
+    layer = 0
+    vc_all = np.zeros((g.num_layers, H, 3), np.int64); vc_all[layer] = vc
+    mtc_all = np.zeros((g.num_layers, H, 6), np.int32); mtc_all[layer] = mtc
+    dp.load(dict(valid_count=vc_all, merge_token_count=mtc_all))
+    assert len(t_list) * H > 64
+    remap = (1, 18, 21, 0)
+    o, total = run_plan(dp, to_dev(host), layer, t_list, remap)
+    want = O.plan_multi(g, host, vc, mtc, t_list, *remap)
+    for name, w in zip(["cu", "sk", "sg", "sl", "dst", "traw", "tremap"], want[:7]):
+        assert (to_np(o[name]) == w).all(), name
+    assert int(total.item()) == want[7]
+
+
 def _tables_dev(tables):
     return tuple(torch.from_numpy(t).to(DEV) for t in tables)
 
