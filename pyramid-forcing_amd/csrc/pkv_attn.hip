@@ -12,6 +12,9 @@
 // row-major into LDS with 16-byte stores.  Each staged tile serves 256 query
 // rows, which halves the load and LDS-store traffic per flop of a 128-row
 // workgroup.  The order of the work items balances the XCDs (balanced_item).
+// In a sequence's last, partial query tile the waves without query rows only
+// stage their share of the tiles, which leaves their SIMDs' matrix cores and
+// the LDS read bandwidth to the waves that have rows.
 //
 // Software pipelining.  Iteration j computes S(j+1) = K(j+1) Q^T while the
 // softmax of S(j), computed one iteration earlier, runs in the same basic
@@ -249,6 +252,10 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
   const int lane = tid & 63, wave = tid >> 6;
   const int lq = lane & 31, hf = lane >> 5;
   const int row_q = q0 + wave * 32 + lq;
+  // the wave holds query rows (a partial last query tile leaves the later
+  // waves without any); decided on a scalar copy of the wave index, so the
+  // branch is uniform
+  const bool wave_rows = q0 + __builtin_amdgcn_readfirstlane(wave) * 32 < Lq;
   const float c = p.scale_log2;
 
   // ---- Q^T operand, resident for the whole key loop
@@ -398,35 +405,51 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
     load_v(2, sv[1]);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    f32x16 sa0 = qk(0, 0), sa1 = qk(0, 1), sb0, sb1;
-    mask(sa0, sa1, 0);
-    m = tile_max(sa0, sa1);  // finite: the first tile holds key 0
     bool ovf = false;
+    if (wave_rows) {
+      f32x16 sa0 = qk(0, 0), sa1 = qk(0, 1), sb0, sb1;
+      mask(sa0, sa1, 0);
+      m = tile_max(sa0, sa1);  // finite: the first tile holds key 0
 
-    // iteration j: Ks[(j+1)%2] = K(j+1), Vs[j%2] = V(j), (c0, c1) = S(j);
-    // register set j%2 holds (K(j+2), V(j+1)), stored now, then refilled
-    // with (K(j+4), V(j+3)); S(j+1) is computed while S(j) goes through the
-    // exponentials, then O += V(j)^T P(j)
-    auto step = [&](int j, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1, uint4 (&k4)[LD],
-                    uint4 (&v4)[LD]) {
-      __syncthreads();
-      store_k(j & 1, k4);
-      store_v((j + 1) & 1, v4);
-      load_k(j + 4, k4);
-      load_v(j + 3, v4);
-      mask(c0, c1, j * kBK);
-      // ---- one block: S(j+1) MFMAs interleaved with the exponentials of S(j)
-      n0 = qk((j + 1) & 1, 0);
-      n1 = qk((j + 1) & 1, 1);
-      bf16x8 pb[4];
-      const float ps = probs(c0, c1, m, pb);
-      l += ps;
-      ovf |= !(ps < exp2f(kHeadroom));
-      pv(j & 1, pb);
-    };
-    for (int pr = 0; pr < n_pairs; ++pr) {
-      step(2 * pr, sa0, sa1, sb0, sb1, sk[0], sv[0]);
-      step(2 * pr + 1, sb0, sb1, sa0, sa1, sk[1], sv[1]);
+      // iteration j: Ks[(j+1)%2] = K(j+1), Vs[j%2] = V(j), (c0, c1) = S(j);
+      // register set j%2 holds (K(j+2), V(j+1)), stored now, then refilled
+      // with (K(j+4), V(j+3)); S(j+1) is computed while S(j) goes through the
+      // exponentials, then O += V(j)^T P(j)
+      auto step = [&](int j, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1, uint4 (&k4)[LD],
+                      uint4 (&v4)[LD]) {
+        __syncthreads();
+        store_k(j & 1, k4);
+        store_v((j + 1) & 1, v4);
+        load_k(j + 4, k4);
+        load_v(j + 3, v4);
+        mask(c0, c1, j * kBK);
+        // ---- one block: S(j+1) MFMAs interleaved with the exponentials of S(j)
+        n0 = qk((j + 1) & 1, 0);
+        n1 = qk((j + 1) & 1, 1);
+        bf16x8 pb[4];
+        const float ps = probs(c0, c1, m, pb);
+        l += ps;
+        ovf |= !(ps < exp2f(kHeadroom));
+        pv(j & 1, pb);
+      };
+      for (int pr = 0; pr < n_pairs; ++pr) {
+        step(2 * pr, sa0, sa1, sb0, sb1, sk[0], sv[0]);
+        step(2 * pr + 1, sb0, sb1, sa0, sa1, sk[1], sv[1]);
+      }
+    } else {
+      // no query row in this wave: stage its share of every tile, with the
+      // same barriers as the steps above
+      for (int pr = 0; pr < n_pairs; ++pr) {
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+          const int j = 2 * pr + hs;
+          __syncthreads();
+          store_k(j & 1, sk[hs]);
+          store_v((j + 1) & 1, sv[hs]);
+          load_k(j + 4, sk[hs]);
+          load_v(j + 3, sv[hs]);
+        }
+      }
     }
     if (ovf) ovf_any = 1;
     __syncthreads();
@@ -447,6 +470,7 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
         store_k(0, sk[0]);
         store_v(0, sv[0]);
         __syncthreads();
+        if (!wave_rows) continue;
         f32x16 c0 = qk(0, 0), c1 = qk(0, 1);
         mask(c0, c1, kt * kBK);
         const float m_new = fmaxf(m, tile_max(c0, c1));
