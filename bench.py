@@ -40,7 +40,7 @@ ATTN_KERNEL = "attn_fwd_kernel<128>"
 # counter reads for a 1 GiB device-to-device copy (FETCH_SIZE x 2.000,
 # WRITE_SIZE x 1.000); profiles/hbm_traffic_counters.md lists the runs.
 TRAFFIC_BYTES = {
-    "attn_fwd_kernel<128>": 5673.03e6 + 431.31e6,   # config 2, one launch (30 x 12 sequences)
+    "attn_fwd_kernel<128>": 11000.97e6 + 431.31e6,  # config 2, one launch (30 x 12 sequences)
     "pack_kernel": 305.15e6 + 296.94e6,             # config 3, one layer call (mean over 273 launches)
     "merge_accum_kernel": 13.57e6 + 5.70e6,         # config 4, one eviction (mean over 200 launches)
 }
