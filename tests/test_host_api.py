@@ -127,7 +127,21 @@ def test_map_dynamic_pos_time_modes():
 
 REQUIRED_OPS = ["pyramidkv_pack", "pyramidkv_update", "mega_state_update", "mega_plan", "mega_plan_multi",
                 "mega_state_perhead_size", "mega_merge_accum", "mega_merge_accum_weighted", "ragged_attention",
-                "rope_apply", "cache_update", "update_descriptors"]
+                "rope_apply", "cache_update", "update_descriptors", "mega_attend_kv", "dit_layer_norm", "dit_rms_norm",
+                "dit_residual_", "dit_gelu_tanh", "dit_residual_layer_norm_"]
+
+
+def test_dit_row_ops_meta_shapes():
+    """The DiT row ops' Meta registrations give the output shapes and dtypes
+    (shape inference without a device)."""
+    ops = _ops.ops()
+    x = torch.empty(7, 256, device="meta")
+    y = torch.empty(7, 256, dtype=torch.bfloat16, device="meta")
+    out = ops.dit_residual_layer_norm_(x, y, None, None, None, True, 1e-6)
+    assert out.shape == (7, 256) and out.dtype == torch.bfloat16 and out.device.type == "meta"
+    out = ops.dit_layer_norm(x, None, None, True, 1e-6)
+    assert out.shape == (7, 256) and out.dtype == torch.bfloat16
+    assert ops.dit_gelu_tanh(y).shape == (7, 256)
 
 
 def test_torch_ops_surface_registered():
