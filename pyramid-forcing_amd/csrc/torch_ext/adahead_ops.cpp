@@ -48,7 +48,7 @@ static void check_i32(const Tensor &t, const char *name) {
 constexpr int64_t kMaxMergeBlocks = 6, kMaxMergeActive = 2, kMaxMergeTokens = 420;
 
 // ---------------------------------------------------------------------------
-// PyramidKVCacheManager (pyramidkv_manager.h:62-199, .cc:237-415)
+// PyramidKVCacheManager (pyramidkv_manager.h:62-199, .cc:36-214)
 // ---------------------------------------------------------------------------
 class PyramidKVCacheManager : public torch::CustomClassHolder {
  public:
@@ -113,7 +113,7 @@ class PyramidKVCacheManager : public torch::CustomClassHolder {
     acc_wsum_ = at::zeros({L, H, MMA}, of);
   }
 
-  void reset() {  // pyramidkv_manager.cc:361-380
+  void reset() {  // pyramidkv_manager.cc:160-179
     write_idx_.zero_();
     valid_count_.zero_();
     head_t_.fill_(-1);
@@ -125,7 +125,7 @@ class PyramidKVCacheManager : public torch::CustomClassHolder {
     acc_ng_.zero_();
   }
 
-  void set_strategy(int64_t layer_idx, int64_t head_idx, int64_t kind, Tensor params) {  // .cc:382-415
+  void set_strategy(int64_t layer_idx, int64_t head_idx, int64_t kind, Tensor params) {  // .cc:181-214
     TORCH_CHECK(layer_idx >= 0 && layer_idx < L_, "PyramidKVCacheManager::set_strategy layer_idx out of range");
     TORCH_CHECK(head_idx >= 0 && head_idx < H_, "PyramidKVCacheManager::set_strategy head_idx out of range");
     TORCH_CHECK(params.dtype() == at::kChar, "PyramidKVCacheManager::set_strategy params must be int8");

@@ -1,61 +1,36 @@
-"""Head compositions and middle-strategy parameter records.
+"""Per-head cache composition records.
 
-``HeadComposition`` mirrors the reference's per-head record
-(pyramidkv/base.py:79-110): sink frames + middle strategies + recent
-frames.  The strategy classes carry the parameters the device path encodes
-into the per-head state record (pyramidkv/cyclic.py:25-28, stride.py:27-30,
-lag.py:25-33, merge.py:44-48, recent.py:12); the reference's Python-side
-per-frame update/collect of the non-MegaCache cache is not part of this
-package.
+``HeadComposition`` is the reference's per-head record (pyramidkv/base.py:79-110):
+sink frames, a union of middle strategies and recent frames.  The middle
+strategies (cyclic.py, stride.py, lag.py, merge.py, recent.py) are
+parameter records: the device path encodes them into the 600-byte per-head
+state record, and the state machine on the GPU does the per-frame work the
+reference's Python strategy objects do in its AdaptiveKVCache path.
+``FrameAnchor`` is the reference's raw-anchor payload type
+(pyramidkv/base.py:16-23), kept for callers that construct or annotate with it.
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass
+class FrameAnchor:
+    """One stored frame: raw K, V, positions and its latent time t."""
+
+    k: torch.Tensor
+    v: torch.Tensor
+    pos: torch.Tensor
+    t: int
+
 
 class MiddleStrategy:
+    """Base of the middle-segment parameter records.  ``dynamic_rope``: the
+    frames' temporal RoPE index is remapped at readout."""
+
     dynamic_rope: bool = True
-
-
-class CyclicStrategy(MiddleStrategy):
-    """Wave: periodic sampling, one ring of ``bucket_cap`` frames per phase."""
-
-    def __init__(self, period: int = 6, bucket_cap: int = 1, dynamic_rope: bool = True):
-        self.period = max(1, int(period))
-        self.bucket_cap = max(1, int(bucket_cap))
-        self.dynamic_rope = bool(dynamic_rope)
-
-
-class StrideStrategy(MiddleStrategy):
-    """Anchor: keep frames with t % interval == 0 in a FIFO of ``capacity``."""
-
-    def __init__(self, interval: int = 6, capacity: int = -1, dynamic_rope: bool = True):
-        self.interval = max(1, int(interval))
-        self.capacity = int(capacity)
-        self.dynamic_rope = bool(dynamic_rope)
-
-
-class LagStrategy(MiddleStrategy):
-    def __init__(self, offsets: list[int] | None = None, history_frames: int = 21, dynamic_rope: bool = False):
-        raw = offsets if offsets is not None else [6]
-        self.offsets = sorted(set(o for o in raw if o > 0))
-        self.history_frames = max(1, int(history_frames))
-        self.dynamic_rope = bool(dynamic_rope)
-
-
-class MergeStrategy(MiddleStrategy):
-    """Veil: fold blocks of patch_size**2 frames into patch x patch means."""
-
-    def __init__(self, patch_size: int = 2, capacity: int = 1, dynamic_rope: bool = True):
-        self.patch_size = max(1, int(patch_size))
-        self.capacity = -1 if int(capacity) < 0 else max(1, int(capacity))
-        self.dynamic_rope = bool(dynamic_rope)
-        self.block_frames = self.patch_size * self.patch_size
-
-
-class RecentStrategy(MiddleStrategy):
-    """No middle anchors: sink + recent only."""
-
-    def __init__(self):
-        self.dynamic_rope = False
 
 
 class HeadComposition:

@@ -13,7 +13,11 @@ import csv
 import os
 from collections.abc import Mapping, Sequence
 
-from .base import CyclicStrategy, HeadComposition, LagStrategy, MergeStrategy, StrideStrategy
+from .base import HeadComposition
+from .cyclic import CyclicStrategy
+from .lag import LagStrategy
+from .merge import MergeStrategy
+from .stride import StrideStrategy
 
 HEAD_LABEL_MAP = {-1: "oscillating", 1: "stable", 2: "stable_sparse"}
 

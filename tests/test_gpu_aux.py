@@ -180,3 +180,47 @@ def test_packed_cache_update_and_readout():
                 assert torch.equal(seg[s], allk[fidx, h])
     cache.reset()
     assert int(cache.manager.valid_count().abs().sum()) == 0
+
+
+def test_packed_cache_ring_partial_and_oversized_calls():
+    """Calls of 1, 3 and 6 frames into a 4-slot ring (the 6-frame call wraps
+    the ring one and a half times), a partially filled layer, and a reset
+    that restarts the ring at slot 0: every head's readout equals the last
+    min(n, 4) frames written to it, in ring-slot order (slot = n % 4)."""
+    from pyramidkv.packed_cache import PyramidKVPackedCache
+    L, H, D, FS, R = 2, 2, 64, 8, 4
+    cache = PyramidKVPackedCache(L, H, D, FS, max_recent_frames=R, device=DEV)
+    written = [[], []]
+
+    def put(layer, n):
+        k = torch.randn(n, H, FS, D, device=DEV).to(torch.bfloat16)
+        v = torch.randn(n, H, FS, D, device=DEV).to(torch.bfloat16)
+        cache.update(layer, k, v)
+        written[layer].extend((k[i], v[i]) for i in range(n))
+
+    def check():
+        out = cache.readout()
+        cu = out.cu_seqlens_k.cpu().tolist()
+        for layer in range(L):
+            n = len(written[layer])
+            held = min(n, R)
+            slots = {i % R: written[layer][i] for i in range(n - held, n)}
+            for h in range(H):
+                q = layer * H + h
+                assert cu[q + 1] - cu[q] == held * FS
+                kk = out.k_flat[cu[q]:cu[q + 1]].view(held, FS, D)
+                vv = out.v_flat[cu[q]:cu[q + 1]].view(held, FS, D)
+                for s in range(held):
+                    assert torch.equal(kk[s], slots[s][0][h]) and torch.equal(vv[s], slots[s][1][h])
+
+    put(0, 1)
+    put(1, 3)
+    check()
+    put(0, 6)
+    put(1, 1)
+    check()
+    assert cache.manager.write_idx()[:, :, 2].cpu().tolist() == [[3, 3], [0, 0]]
+    cache.reset()
+    written = [[], []]
+    put(0, 2)
+    check()

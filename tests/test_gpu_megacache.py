@@ -202,7 +202,7 @@ def _states(cache, H):
 
 
 def test_reference_noisy_iterations_then_clean_commits():
-    from pyramidkv.base import HeadComposition, StrideStrategy
+    from pyramidkv import HeadComposition, StrideStrategy
     H, D, FSEQ, F = 1, 16, 4, 3
     cache = _single_head_caches(HeadComposition("stride", 1, 3, 4, [StrideStrategy(interval=1, capacity=8)]))[0]
     torch.manual_seed(7)
@@ -221,7 +221,7 @@ def test_reference_noisy_iterations_then_clean_commits():
 
 
 def test_reference_block_2_noisy_uses_block_1_committed_baseline():
-    from pyramidkv.base import HeadComposition, StrideStrategy
+    from pyramidkv import HeadComposition, StrideStrategy
     H, D, FSEQ, F = 1, 16, 4, 3
     cache = _single_head_caches(HeadComposition("stride", 1, 3, 4, [StrideStrategy(interval=1, capacity=8)]))[0]
     torch.manual_seed(11)
@@ -238,7 +238,7 @@ def test_reference_block_2_noisy_uses_block_1_committed_baseline():
 
 
 def test_reference_recent_fifo_no_noisy_contamination():
-    from pyramidkv.base import HeadComposition, RecentStrategy
+    from pyramidkv import HeadComposition, RecentStrategy
     H, D, FSEQ, F = 1, 16, 4, 3
     cache = _single_head_caches(HeadComposition("recent_only", -1, 1, 4, [RecentStrategy()]), max_sink=1)[0]
     torch.manual_seed(101)

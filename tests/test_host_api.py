@@ -14,7 +14,7 @@ from pyramidkv import _mega_state_ops as S
 from pyramidkv import _mega_state_ref as R
 from pyramidkv import _ops, factory
 from pyramidkv._mega_cache import _composition_to_perhead_state
-from pyramidkv.base import CyclicStrategy, HeadComposition, LagStrategy, MergeStrategy, StrideStrategy
+from pyramidkv import CyclicStrategy, HeadComposition, LagStrategy, MergeStrategy, StrideStrategy
 from pyramidkv.rope import flat_freq_parts, map_dynamic_pos_time, map_sink_time, wan_freqs
 
 

@@ -11,7 +11,7 @@ import numpy as np
 from oracle import oracle as O
 from pyramidkv import _mega_state_ops as S
 from pyramidkv._mega_cache import _composition_to_perhead_state
-from pyramidkv.base import HeadComposition, RecentStrategy, StrideStrategy
+from pyramidkv import HeadComposition, RecentStrategy, StrideStrategy
 
 
 def _ref_cache(comps_row, D=16, FS=4, max_sink=3, max_middle=8, max_recent=4, W=2):

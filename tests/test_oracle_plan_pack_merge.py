@@ -13,6 +13,12 @@
 * Merge: the reference's vectors from tests/test_mega_merge_accum_cuda.py
   (55-288: per-token means, 2x2 patch means, counts, group positions) and a
   bit-exact sequential-float32 restatement for the accumulation order.
+* Weighted merge (config 4): the float64 closed form sum(w x) / (count *
+  sum(w)) per patch group, for blocks spanning several calls; the planted
+  mistakes (w applied twice, count * frames divisor) fail the same bar.
+* attention_ref: closed forms (uniform keys, one dominant key, two-key
+  logistic weights, the scale) and the sequence selection of the ragged
+  layouts.
 """
 import numpy as np
 import pytest
@@ -327,3 +333,190 @@ def test_merge_weighted_unit_weights_equal_reference():
     assert (a["mk"] == b["mk"]).all() and (a["mv"] == b["mv"]).all()
     _, _, c = _drive_merge(H, FSEQ, D, [0, 1, 2, 3], pos, 9, weights=np.array([0.5, 1, 0.25, 1], np.float32))
     assert not (a["mk"] == c["mk"]).all()
+
+
+def _weighted_rollout(H, D, W, rows, calls, weights, seed):
+    """Drive the oracle's state machine + merge accumulate over consecutive
+    clean calls (frame lists in `calls`, per-frame weights in `weights`) on
+    a regular rows x W grid; returns the frames, the per-call finalize
+    descriptors and the accumulator dict."""
+    FSEQ = rows * W
+    states = O.states_to_bytes([O.make_merge(2, 6) for _ in range(H)])
+    acc = _merge_layer_arrays(H, FSEQ, D)
+    rng = np.random.default_rng(seed)
+    frames, fins = {}, []
+    for ts in calls:
+        F = len(ts)
+        desc = O.state_update(states, ts, 1)
+        pos = np.zeros((F, H, FSEQ, 3), np.int64)
+        pos[..., 0] = np.array(ts).reshape(F, 1, 1)
+        pos[..., 1] = np.arange(FSEQ) // W
+        pos[..., 2] = np.arange(FSEQ) % W
+        nk = O.f32_to_bf16(rng.standard_normal((F, H, FSEQ, D)).astype(np.float32))
+        nv = O.f32_to_bf16(rng.standard_normal((F, H, FSEQ, D)).astype(np.float32))
+        w = np.array([weights[t] for t in ts], np.float32)
+        O.merge_accum(states, nk, nv, np.ascontiguousarray(pos), desc, acc, w)
+        for i, t in enumerate(ts):
+            frames[t] = (O.bf16_to_f32(nk[i]).astype(np.float64), O.bf16_to_f32(nv[i]).astype(np.float64))
+        fins.append((ts, desc[6].reshape(H, F)))
+    return frames, fins, acc
+
+
+def _closed_form_block(frames, weights, block, W, rows, p=2, wpow=1, divisor="sum_w"):
+    """float64 sum_f w_f * sum_{tok in g} x / (|g| * sum_f w_f) per 2x2 patch
+    group g of `block` (4 frames).  wpow / divisor plant the mistakes the
+    test must reject (w applied twice; count * frames as the divisor)."""
+    ts = list(range(4 * block, 4 * block + 4))
+    ws = np.array([weights[t] for t in ts], np.float64)
+    cols, grows = W // p, rows // p
+    H, FSEQ, D = frames[ts[0]][0].shape
+    out_k = np.zeros((H, grows * cols, D))
+    out_v = np.zeros((H, grows * cols, D))
+    for g in range(grows * cols):
+        gy, gx = divmod(g, cols)
+        toks = [(p * gy + dy) * W + p * gx + dx for dy in range(p) for dx in range(p)]
+        sk = sum(ws[i] ** wpow * frames[t][0][:, toks].sum(1) for i, t in enumerate(ts))
+        sv = sum(ws[i] ** wpow * frames[t][1][:, toks].sum(1) for i, t in enumerate(ts))
+        div = len(toks) * (ws.sum() if divisor == "sum_w" else len(ts))
+        out_k[:, g], out_v[:, g] = sk / div, sv / div
+    return out_k, out_v
+
+
+def test_merge_weighted_closed_form_across_calls():
+    """config-4's running weighted average: every finalized anchor equals
+    sum(w x) / (count * sum(w)) of its block in float64 within the north
+    star's 2e-2 / 2e-3, with blocks that span several calls (weights and
+    their running sum carried between calls).  The reference operation is
+    the w == 1 case (mega_merge_accum.cu:193-249)."""
+    H, D, W, rows = 3, 16, 8, 6
+    rng = np.random.default_rng(123)
+    weights = {t: float(np.float32(rng.uniform(0.1, 1.0))) for t in range(8)}
+    calls = [[0], [1, 2], [3, 4], [5, 6, 7]]
+    frames, fins, acc = _weighted_rollout(H, D, W, rows, calls, weights, seed=4)
+    done = {}
+    for ts, fin in fins:
+        for i, t in enumerate(ts):
+            for h in range(H):
+                if fin[h, i] >= 0:
+                    done.setdefault(t // 4, {})[h] = int(fin[h, i])
+    assert sorted(done) == [0, 1]
+    ng = (rows // 2) * (W // 2)
+    for block in (0, 1):
+        want_k, want_v = _closed_form_block(frames, weights, block, W, rows)
+        wrong = [_closed_form_block(frames, weights, block, W, rows, wpow=2),
+                 _closed_form_block(frames, weights, block, W, rows, divisor="frames")]
+        for h in range(H):
+            slot = done[block][h]
+            assert acc["mtc"][h, slot] == ng
+            got_k = O.bf16_to_f32(acc["mk"][h, slot, :ng]).astype(np.float64)
+            got_v = O.bf16_to_f32(acc["mv"][h, slot, :ng]).astype(np.float64)
+            for got, want in ((got_k, want_k[h]), (got_v, want_v[h])):
+                err = np.abs(got - want)
+                assert err.max() < 2e-2 and err.mean() < 2e-3, (block, h, err.max(), err.mean())
+            # the planted mistakes fail the same bar
+            for wk, wv in wrong:
+                e = np.abs(got_k - wk[h])
+                assert e.max() >= 2e-2 or e.mean() >= 2e-3
+            assert acc["mpos"][h, slot, 0].tolist() == [4 * block, 0, 0]
+
+
+def test_merge_weighted_single_frame_calls_and_unit_weight_block():
+    """40 single-frame calls (the config-4 eviction pattern, 10 blocks):
+    each anchor against the float64 weighted mean; a block whose weights
+    are all 1 reduces to the plain mean."""
+    H, D, W, rows = 2, 8, 4, 4
+    rng = np.random.default_rng(77)
+    weights = {t: float(np.float32(rng.uniform(0.1, 1.0))) for t in range(40)}
+    for t in range(8, 12):
+        weights[t] = 1.0
+    frames, fins, acc = _weighted_rollout(H, D, W, rows, [[t] for t in range(40)], weights, seed=8)
+    ng = (rows // 2) * (W // 2)
+    # which block each anchor slot holds last, from the finalize descriptors
+    # (the completed FIFO's slot-id shift keeps rewriting its last slot)
+    held = {}
+    for ts, fin in fins:
+        for h in range(H):
+            if fin[h, 0] >= 0:
+                held[(h, int(fin[h, 0]))] = ts[0] // 4
+    assert len(held) == 6 * H and sorted(set(held.values())) == [0, 1, 2, 3, 4, 9]
+    for (h, slot), block in held.items():
+        want_k, _ = _closed_form_block(frames, weights, block, W, rows)
+        got = O.bf16_to_f32(acc["mk"][h, slot, :ng]).astype(np.float64)
+        err = np.abs(got - want_k[h])
+        assert err.max() < 2e-2 and err.mean() < 2e-3
+        assert acc["mpos"][h, slot, 0, 0] == 4 * block
+    # the unit-weight block (t = 8..11) was evicted from the FIFO; rerun it alone
+    frames1, _, acc1 = _weighted_rollout(H, D, W, rows, [[8], [9], [10], [11]],
+                                         {t: 1.0 for t in range(8, 12)}, seed=8)
+    k = np.stack([frames1[t][0] for t in range(8, 12)])  # [4, H, FSEQ, D]
+    plain = k.reshape(4, H, rows // 2, 2, W // 2, 2, D).transpose(1, 2, 4, 0, 3, 5, 6)
+    plain = plain.reshape(H, ng, 16, D).mean(2)
+    got = O.bf16_to_f32(acc1["mk"][:, 0, :ng]).astype(np.float64)
+    assert np.abs(got - plain).max() < 2e-2
+
+
+def test_attention_ref_closed_forms():
+    """attention_ref against what the mathematics fixes: identical keys give
+    the mean of V; one key that outscores the rest by a wide margin gives its
+    V row; two keys give the logistic weights; the scale multiplies the
+    logits; an empty key set gives zeros."""
+    rng = np.random.default_rng(3)
+    D, Lq, Lk = 16, 5, 9
+    q = rng.standard_normal((Lq, D))
+    v = rng.standard_normal((Lk, D))
+    k_same = np.tile(rng.standard_normal((1, D)), (Lk, 1))
+    out = O.attention_ref(q, k_same, v)
+    assert np.abs(out - v.mean(0)).max() < 1e-12
+    # a dominant key: logits 60 units above every other key -> weight 1 - O(e^-60)
+    k = rng.standard_normal((Lk, D)) * 0.01
+    qd = np.zeros((Lq, D))
+    qd[:, 0] = 1.0
+    k[4, 0] = 60.0 * np.sqrt(D)
+    assert np.abs(O.attention_ref(qd, k, v) - v[4]).max() < 1e-12
+    # two keys: p1 = 1 / (1 + exp(s2 - s1)) with s = q.k / sqrt(D)
+    k2, v2 = rng.standard_normal((2, D)), rng.standard_normal((2, D))
+    s = q @ k2.T / np.sqrt(D)
+    p1 = 1.0 / (1.0 + np.exp(s[:, 1] - s[:, 0]))
+    want = p1[:, None] * v2[0] + (1 - p1)[:, None] * v2[1]
+    assert np.abs(O.attention_ref(q, k2, v2) - want).max() < 1e-12
+    # the scale multiplies q.k: scale c with q equals the default scale with q * c * sqrt(D)
+    kk = rng.standard_normal((Lk, D))
+    c = 0.37
+    a = O.attention_ref(q, kk, v, scale=c)
+    b = O.attention_ref(q * c * np.sqrt(D), kk, v)
+    assert np.abs(a - b).max() < 1e-12
+    assert not np.allclose(a, O.attention_ref(q, kk, v))
+    assert (O.attention_ref(q, np.zeros((0, D)), np.zeros((0, D))) == 0).all()
+
+
+def test_ragged_attention_ref_sequence_indexing():
+    """Each (batch, head) sequence's V is a constant vector c(b, h), so its
+    output is exactly c(b, h) whatever the weights: this pins which key rows
+    the per-head (cu_k[b*Hq + h]) and shared (cu_k[b]) layouts select."""
+    rng = np.random.default_rng(5)
+    D, Hq = 8, 3
+    cu_q = np.array([0, 4, 7, 12])
+    lens = rng.integers(1, 6, len(cu_q) - 1)
+    q = rng.standard_normal((cu_q[-1], Hq, D))
+    # per-head ragged KV
+    seq_lens = rng.integers(1, 7, (len(cu_q) - 1) * Hq)
+    cu_k = np.concatenate([[0], np.cumsum(seq_lens)])
+    k = rng.standard_normal((cu_k[-1], D))
+    v = np.zeros((cu_k[-1], D))
+    for s in range(len(seq_lens)):
+        v[cu_k[s]:cu_k[s + 1]] = s + 1.0
+    out = O.ragged_attention_ref(q, k, v, cu_q, cu_k, heads_q=Hq, kv_per_head=True)
+    for b in range(len(cu_q) - 1):
+        for h in range(Hq):
+            assert np.abs(out[cu_q[b]:cu_q[b + 1], h] - (b * Hq + h + 1.0)).max() < 1e-12
+    # shared KV per batch, [total_k, Hq, D] (flash-attn varlen layout)
+    cu_kb = np.concatenate([[0], np.cumsum(lens)])
+    kb = rng.standard_normal((cu_kb[-1], Hq, D))
+    vb = np.zeros((cu_kb[-1], Hq, D))
+    for b in range(len(lens)):
+        for h in range(Hq):
+            vb[cu_kb[b]:cu_kb[b + 1], h] = 10.0 * b + h
+    out = O.ragged_attention_ref(q, kb, vb, cu_q, cu_kb, heads_q=Hq, kv_per_head=False)
+    for b in range(len(cu_q) - 1):
+        for h in range(Hq):
+            assert np.abs(out[cu_q[b]:cu_q[b + 1], h] - (10.0 * b + h)).max() < 1e-12
