@@ -162,6 +162,26 @@ int pkv_merge_accum(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ,
                     const float *frame_weights, const pkv_merge_layer *ml,
                     void *workspace, pkv_stream_t stream);
 
+/* pkv_merge_accum without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * scratch is a static device array of PKV_MERGE_STATIC_SCRATCH_BYTES per
+ * device (held until the process ends); calls needing more
+ * (pkv_merge_workspace_size(H, F, FSEQ, MTPA) above the limit: about H * F
+ * <= 130 at FSEQ 1560) return PKV_ERR_CAPACITY.  Same kernels and results as
+ * pkv_merge_accum.  Calls that overlap on one device race on the array. */
+#define PKV_MERGE_STATIC_SCRATCH_BYTES (1 << 20)
+
+int pkv_merge_accum_static(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ,
+                           int32_t D, int32_t MMA, int32_t MMB, int32_t MTPA,
+                           const uint16_t *new_k, const uint16_t *new_v,
+                           const int64_t *new_pos, const int32_t *desc_dst_kind,
+                           const int32_t *desc_merge_accum_slot,
+                           const int32_t *desc_merge_finalize_completed_idx,
+                           const int32_t *desc_merge_is_new_block,
+                           const float *frame_weights, const pkv_merge_layer *ml,
+                           pkv_stream_t stream);
+
 /* Dynamic-RoPE remap configuration (mega_plan.cc:63-114). */
 typedef struct pkv_remap {
   int32_t sink_mode_code;      /* 0 lag, 1 window_clamp */

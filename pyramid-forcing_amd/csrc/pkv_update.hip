@@ -13,6 +13,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "pkv_common.h"
 #include "pkv_state_machine.h"
 
@@ -1054,6 +1056,39 @@ static int launch_merge(const MergeArgs &ma, hipStream_t st) {
   return launch_merge_accum(ma, st);
 }
 
+// Scratch of pkv_merge_accum_static: the per-(head, frame) merge snapshots
+// (MergeWs) in a file-scope device array, for callers that cannot allocate.
+// Each device holds its own copy at its own address; host code never uses
+// the symbol itself, only the address hipGetSymbolAddress returns for the
+// current device, looked up once per device.  Every snapshot entry the
+// accumulate launch reads is written by the preparation launch of the same
+// call, so the array needs no clearing between calls; calls that overlap on
+// one device (two streams) race on it.
+static __device__ __align__(256) uint8_t scratch[PKV_MERGE_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+
+static int merge_scratch_device_ptr(void **out) {
+  static std::mutex mu;
+  static void *dev_ptr[kMaxScratchDevices];
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PKV_ERR_HIP, "merge_accum_static: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(PKV_ERR_UNSUPPORTED, "merge_accum_static: device %d beyond %d", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!dev_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(PKV_ERR_HIP, "merge_accum_static: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    dev_ptr[dev] = p;
+  }
+  *out = dev_ptr[dev];
+  return PKV_OK;
+}
+
 static PoolPtrs pool_ptrs(const pkv_geometry *g, const pkv_pools *p) {
   PoolPtrs pp;
   pp.k[0] = p->sink_k; pp.v[0] = p->sink_v; pp.pos[0] = p->sink_pos;
@@ -1148,6 +1183,29 @@ int pkv_merge_accum(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, i
 
 int64_t pkv_merge_workspace_size(int32_t H, int32_t F, int32_t FSEQ, int32_t MTPA) {
   return merge_ws_bytes(H, F, FSEQ, MTPA);
+}
+
+int pkv_merge_accum_static(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t D, int32_t MMA,
+                           int32_t MMB, int32_t MTPA, const uint16_t *new_k, const uint16_t *new_v,
+                           const int64_t *new_pos, const int32_t *desc_dst_kind,
+                           const int32_t *desc_merge_accum_slot,
+                           const int32_t *desc_merge_finalize_completed_idx,
+                           const int32_t *desc_merge_is_new_block, const float *frame_weights,
+                           const pkv_merge_layer *ml, pkv_stream_t stream) {
+  if (H == 0 || F == 0) return PKV_OK;
+  if (H < 0 || F < 0 || FSEQ <= 0 || MTPA <= 0) return fail(PKV_ERR_INVALID, "merge_accum_static: bad arguments");
+  const int64_t need = merge_ws_bytes(H, F, FSEQ, MTPA);
+  if (need > PKV_MERGE_STATIC_SCRATCH_BYTES)
+    return fail(PKV_ERR_CAPACITY,
+                "merge_accum_static: %lld bytes of scratch needed for %d heads x %d frames x %d tokens; "
+                "the static buffer holds %d (use pkv_merge_accum with a workspace)",
+                static_cast<long long>(need), H, F, FSEQ, PKV_MERGE_STATIC_SCRATCH_BYTES);
+  void *ws = nullptr;
+  int rc = merge_scratch_device_ptr(&ws);
+  if (rc) return rc;
+  return pkv_merge_accum(states, H, F, FSEQ, D, MMA, MMB, MTPA, new_k, new_v, new_pos, desc_dst_kind,
+                         desc_merge_accum_slot, desc_merge_finalize_completed_idx, desc_merge_is_new_block,
+                         frame_weights, ml, ws, stream);
 }
 
 static int64_t update_ws_bytes(int H, int F) {

@@ -98,6 +98,8 @@ def lib():
         L.pkv_cache_update_workspace_size.argtypes = [ctypes.POINTER(Geometry), _c_i32]
         L.pkv_merge_workspace_size.restype = _c_i64
         L.pkv_merge_workspace_size.argtypes = [_c_i32] * 4
+        L.pkv_merge_accum_static.argtypes = [_c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32] + \
+            [_c_p] * 10
         _lib = L
     return _lib
 
