@@ -32,18 +32,23 @@ METRIC = "ragged-attn TFLOP/s + cache update/pack GB/s (% roofline); latent chun
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 FSEQ, H, L, D, QTOK = 1560, 12, 30, 128, 4680
-ATTN_KERNEL = "attn_fwd_kernel<128>"
+ATTN_KERNEL = "attn_pp_kernel"
 
-# HBM bytes per launch of each workload's dominant kernel, from two rocprofv3
-# --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) of
-# `bench.py --workload {attn,cache,merge}`, each scaled by what the same
-# counter reads for a 1 GiB device-to-device copy (FETCH_SIZE x 2.000,
-# WRITE_SIZE x 1.000); profiles/hbm_traffic_counters.md lists the runs.
-TRAFFIC_BYTES = {
-    "attn_fwd_kernel<128>": 11000.97e6 + 431.31e6,  # config 2, one launch (30 x 12 sequences)
-    "pack_kernel": 305.15e6 + 296.94e6,             # config 3, one layer call (mean over 273 launches)
-    "merge_accum_kernel": 13.57e6 + 5.70e6,         # config 4, one eviction (mean over 200 launches)
-}
+# HBM bytes per launch of each workload's dominant kernel, measured with two
+# rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE) and kept, with the
+# commands and the copy-kernel calibration, in profiles/hbm_traffic.json /
+# profiles/hbm_traffic_counters.md.  A kernel without an entry there reports
+# traffic null.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def traffic_bytes(kernel: str):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            entry = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+    return float(entry["total_bytes"]) if entry else None
 
 
 def config2_lengths(seed: int = 0):
@@ -543,7 +548,8 @@ def main():
                    "q_tokens_per_head": QTOK, "kv_tokens_mean": round(r["mean_lk"], 1),
                    "kv_tokens_total": int(r["lk"].sum()), "labels_seed": 0, "flop_per_step": r["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": TRAFFIC_BYTES[ATTN_KERNEL],
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic_bytes(ATTN_KERNEL),
+                     "traffic_source": "profiles/hbm_traffic.json",
                      "kernel": ATTN_KERNEL, "avg_launch_ms": round(r["kernel_ms"], 4)},
     }
     if not args.no_cpu_baseline:
@@ -599,7 +605,7 @@ def secondary(args):
         "packed_tokens": c3["pack_tok"], "layers": L, "heads": H, "step": 40, "policy": "shipped best_labels.csv",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "dominant_kernel": "pack_kernel", "dominant_kernel_traffic": TRAFFIC_BYTES["pack_kernel"]},
+                     "dominant_kernel": "pack_kernel", "dominant_kernel_traffic": traffic_bytes("pack_kernel")},
         "plan_pack_layer0": {"ms": round(c3["plan_pack_ms_l0"], 4), "GB/s": round(pk_gbs, 2),
                              "frac": round(pk_gbs / PEAK_HBM_GBS, 4)},
         "parity_layer0_bit_exact": ok, "cpu_baseline": cpu}
@@ -613,7 +619,7 @@ def secondary(args):
         "roofline": {"bound": "hbm", "achieved": round(gbs4, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs4 / PEAK_HBM_GBS, 4), "traffic": None,
                      "dominant_kernel": "merge_accum_kernel",
-                     "dominant_kernel_traffic": TRAFFIC_BYTES["merge_accum_kernel"]},
+                     "dominant_kernel_traffic": traffic_bytes("merge_accum_kernel")},
         "parity_bit_exact": c4["parity"], "graph_replay_matches_eager": c4["graph_same"], "cpu_baseline": c4["cpu"]}
     del c4
     torch.cuda.empty_cache()

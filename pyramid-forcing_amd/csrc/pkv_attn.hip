@@ -1,6 +1,9 @@
 // Ragged-cache attention for gfx950: bf16 inputs, fp32 online softmax and
 // accumulation, MFMA v_mfma_f32_32x32x16_bf16.  Replaces the reference's
 // flash_attn_varlen_func call (pyramidkv/_mega_cache.py:540-559).
+// head_dim 128 runs attn_pp_kernel (two wave groups alternating between
+// matrix work and data movement, described at the kernel); head_dim 64 runs
+// attn_fwd_kernel, described here.
 //
 // Work decomposition.  A workgroup of 8 waves owns 256 query rows (32 per
 // wave) of one (query sequence, head) pair and streams that pair's keys in
@@ -46,6 +49,8 @@
 // exact softmax, with P rounded to bf16 for the P*V product and the row sums
 // taken over the same rounded values (v_dot2c_f32_bf16 against (1, 1)), so
 // numerator and denominator use identical weights.
+
+#include <type_traits>
 
 #include "pkv_common.h"
 
@@ -507,6 +512,400 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Two-group ping-pong kernel (head_dim 128)
+// ---------------------------------------------------------------------------
+// The 8 waves form two groups of four, one wave of each group per SIMD
+// (wave w runs on SIMD w % 4; group 0 = waves 0-3, group 1 = waves 4-7).
+// Keys stream in tiles of 32.  Every tile takes four barrier-separated
+// intervals, and the two groups run the same per-tile program one interval
+// apart, so in every interval one wave of each SIMD issues matrix
+// instructions while the other moves data:
+//
+//   interval    group 0                           group 1
+//   I0          S(t+1) = K(t+1) Q^T, P(t) = exp   K(t+1) LDS -> regs, DMA K(t+4)
+//   I1          V(t) LDS -> regs, DMA K(t+4)      S(t+1), P(t)
+//   I2          O += V(t)^T P(t)                  V(t) LDS -> regs, DMA V(t+3)
+//   I3          K(t+2) LDS -> regs, DMA V(t+3)    O += V(t)^T P(t)
+//
+// The exponentials of P(t) are interleaved with the MFMAs of S(t+1) in the
+// same wave.  K and V tiles reach LDS through buffer loads that write LDS
+// directly (no staging registers), four slots per operand, each slot a
+// separate LDS array so the compiler's wait-count bookkeeping can tell the
+// slots apart.  Each wave copies 4 rows of each tile; rows are 256 bytes
+// with the 16-byte chunks XOR-swizzled (K: chunk ^ (row % 16), V: chunk ^
+// 4 * (row % 4)) so that the fragment reads of 32 rows (K) and the transpose
+// reads of 8 rows (V) spread over all banks.  A wave waits for its own
+// copies (vmcnt) before the barrier that precedes the first read of that
+// tile by any wave.  Softmax, the fast / slow pass split and the operand
+// arrangement are those of attn_fwd_kernel.
+constexpr int kPK = 32;                 // keys per tile
+constexpr int kPRow = 256;              // LDS bytes per key row (128 bf16)
+constexpr int kPTileElems = kPK * 128;  // bf16 elements per tile
+
+typedef __attribute__((address_space(3))) char lds_char;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+// s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
+// lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// workgroup barrier that no instruction is moved across (memory operations
+// by the compiler fence, everything else by the scheduling barriers), so each
+// interval's instructions stay between its two barriers
+__device__ inline void pp_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+}
+
+__global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
+  constexpr int D = 128;
+  __shared__ __attribute__((aligned(16))) uint16_t Ka[kPTileElems], Kb[kPTileElems], Kc[kPTileElems], Kd[kPTileElems];
+  __shared__ __attribute__((aligned(16))) uint16_t Va[kPTileElems], Vb[kPTileElems], Vc[kPTileElems], Vd[kPTileElems];
+  __shared__ __attribute__((aligned(16))) int sched[4 * kSchedMax];
+  auto kslot = [&](auto s) -> uint16_t * {
+    constexpr int S = decltype(s)::value & 3;
+    if constexpr (S == 0) return Ka;
+    else if constexpr (S == 1) return Kb;
+    else if constexpr (S == 2) return Kc;
+    else return Kd;
+  };
+  auto vslot = [&](auto s) -> uint16_t * {
+    constexpr int S = decltype(s)::value & 3;
+    if constexpr (S == 0) return Va;
+    else if constexpr (S == 1) return Vb;
+    else if constexpr (S == 2) return Vc;
+    else return Vd;
+  };
+
+  int seq, qt;
+  const int n_seq = p.n_wg / p.q_tiles;
+  if (n_seq <= kSchedMax) {
+    if (!balanced_item(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, 32 * kWaves, xcd_remap(blockIdx.x, p.n_wg),
+                       sched, seq, qt))
+      return;
+  } else {
+    const int wg = xcd_remap(blockIdx.x, p.n_wg);
+    seq = wg / p.q_tiles;
+    qt = wg % p.q_tiles;
+  }
+  const int b = seq / p.Hq, h = seq % p.Hq;
+  const int q_begin = p.cu_q[b];
+  const int Lq = p.cu_q[b + 1] - q_begin;
+  const int q0 = qt * 32 * kWaves;
+  if (q0 >= Lq) return;
+  const int kv_idx = p.kv_per_head ? seq : b;
+  const int k_begin = p.cu_k[kv_idx];
+  const int Lk = p.cu_k[kv_idx + 1] - k_begin;
+  const uint16_t *qp = p.q + static_cast<int64_t>(q_begin) * p.q_tok + h * p.q_head;
+  const int64_t kv_off = static_cast<int64_t>(k_begin) * p.kv_tok + (p.kv_per_head ? 0 : h * p.kv_head);
+  const uint16_t *kp = p.k + kv_off;
+  const uint16_t *vp = p.v + kv_off;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int grp = wave_s >> 2, wq = wave_s & 3;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int row_q = q0 + wave * 32 + lq;
+  const bool wave_rows = q0 + wave_s * 32 < Lq;
+  const float c = p.scale_log2;
+
+  bf16x8 qr[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row_q < Lq) v = ldg16(qp + static_cast<int64_t>(row_q) * p.q_tok + 16 * s + 8 * hf);
+    qr[s] = as_bf16x8(v);
+  }
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  const int nT = (Lk + kPK - 1) / kPK;
+
+  // ---- tile copies: buffer resources based at the tile's first row and
+  // bounded at the sequence's last row (rows past the end, and tiles past
+  // the end, copy zeros)
+  const int64_t row_elems = p.kv_tok;
+  const int row_bytes = static_cast<int>(row_elems) * 2;
+  // this wave copies rows 16*grp + 4*wq .. +3 of every tile; lane i the
+  // 16-byte position i % 16 of row i / 16 of them
+  const int dma_row = 16 * grp + 4 * wq + (lane >> 4);
+  const int dma_pos = lane & 15;
+  const int k_voff = dma_row * row_bytes + 16 * (dma_pos ^ (dma_row & 15));
+  const int v_voff = dma_row * row_bytes + 16 * (dma_pos ^ (4 * (dma_row & 3)));
+  const int dma_lds = (16 * grp + 4 * wq) * kPRow;
+  // The copies are issued as inline assembly: the compiler then inserts no
+  // wait of its own before the LDS reads of the slots (its bookkeeping
+  // cannot follow the slots around the loop and waits far too early).  Every
+  // wait for them is explicit; the compiler's waits for its own loads stay
+  // correct, since those only ever have more, not fewer, loads after them.
+  auto dma = [&](const uint16_t *base, int kt, uint16_t *slot, int voff) {
+    const int64_t first = static_cast<int64_t>(kt) * kPK;
+    const int64_t left = (static_cast<int64_t>(Lk) - first) * row_elems * 2;
+    const int nrec = static_cast<int>(left <= 0 ? 0 : (left < 0x7fffffff ? left : 0x7fffffff));
+    const uint64_t addr = reinterpret_cast<uint64_t>(base + (left <= 0 ? 0 : first * row_elems));
+    i32x4 rsrc;
+    rsrc[0] = static_cast<int>(addr & 0xffffffffu);
+    rsrc[1] = static_cast<int>((addr >> 32) & 0xffffu);
+    rsrc[2] = nrec;
+    rsrc[3] = kRsrcWord3;
+    const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)slot)) + dma_lds;
+    // m0 is reserved to the compiler, which uses it nowhere else in this
+    // kernel (the listing has no other m0 access)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+  };
+  auto dma_k = [&](uint16_t *slot, int kt) { dma(kp, kt, slot, k_voff); };
+  auto dma_v = [&](uint16_t *slot, int kt) { dma(vp, kt, slot, v_voff); };
+
+  // ---- fragment reads
+  // K: step s reads row lq, 16-byte chunk 2s + hf (swizzled)
+  int kaddr[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) kaddr[s] = lq * kPRow + 16 * ((2 * s + hf) ^ (lq & 15));
+  // V^T: key row 4*hf + (lane%16)/4 (+8, +16*ks), dims 32*db + v_col..+3
+  const int v_row = 4 * hf + ((lane & 15) >> 2);
+  const int v_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int vaddr[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+    vaddr[db] = v_row * kPRow + 16 * ((4 * db + v_col / 8) ^ (4 * (v_row & 3))) + 2 * (v_col % 8);
+  uint4 kreg[8];
+  i16x4 vreg[2][4][2];
+  auto load_k = [&](const uint16_t *slot) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      kreg[s] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(slot) + kaddr[s]);
+  };
+  auto load_v = [&](const uint16_t *slot) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint16_t *ptr = reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(slot) + vaddr[db] +
+                                                                 ks * 16 * kPRow);
+        vreg[ks][db][0] = lds_tr16(ptr);
+        vreg[ks][db][1] = lds_tr16(ptr + 8 * kPRow / 2);
+      }
+  };
+  // S^T of the 32 keys in kreg
+  auto gemm0 = [&](f32x16 &acc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kreg[s]), qr[s], acc, 0, 0, 0);
+  };
+  // O^T += V^T P^T
+  auto gemm1 = [&](const bf16x8 (&pb)[2]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const i16x4 a8[2] = {vreg[ks][db][0], vreg[ks][db][1]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a8), pb[ks], o[db], 0, 0, 0);
+      }
+  };
+  // keys past the sequence's end in the tile at key kb0 -> -inf
+  // (a branch the compiler does not flatten: the volatile asm cannot be
+  // speculated, so full tiles skip the compares)
+  auto mask = [&](f32x16 &s, int kb0) {
+    if (kb0 + kPK > Lk) {
+      asm volatile("");
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (kb0 + 8 * (i / 4) + 4 * hf + (i % 4) >= Lk) s[i] = -INFINITY;
+    }
+  };
+  auto tile_max = [&](const f32x16 &s) {
+    float mq[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mq[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
+    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c;
+  };
+  // P = 2^(S*c - mr) as the two 16-key B operands; returns the lane's sum
+  auto probs = [&](const f32x16 &s, float mr, bf16x8 (&pb)[2]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -mr)));
+    return bf16x8_sum(pb[0], 0.0f) + bf16x8_sum(pb[1], 0.0f);
+  };
+
+  __shared__ int ovf_any;
+  if (tid == 0) ovf_any = 0;
+  bool ovf = false;
+  if (nT > 0) {
+    // prologue: copies of K0, K1, V0, K2, V1, K3, V2 (the order in which the
+    // loop's iterations -4 .. -1 would have issued them), S(0), m and K(1)
+    dma_k(Ka, 0);
+    dma_k(Kb, 1);
+    dma_v(Va, 0);
+    dma_k(Kc, 2);
+    dma_v(Vb, 1);
+    dma_k(Kd, 3);
+    wait_vm<4>();
+    __syncthreads();  // ovf_any initialised, K0 and K1 complete
+    f32x16 sa, sb;
+    if (wave_rows) {
+      load_k(Ka);
+      gemm0(sa);
+      mask(sa, 0);
+      m = tile_max(sa);  // finite: the first tile holds key 0
+      load_k(Kb);
+    }
+    dma_v(Vc, 2);
+    wait_vm<4>();  // V0 complete
+    pp_barrier();
+    // group 1 runs every interval one barrier later than group 0
+    if (grp == 1) pp_barrier();
+
+    bf16x8 pb[2];
+    auto iter = [&](auto tt_c, int t) {
+      constexpr int TT = decltype(tt_c)::value;
+      f32x16 &scur = (TT & 1) ? sb : sa;
+      f32x16 &snext = (TT & 1) ? sa : sb;
+      // I0: S(t+1) MFMAs with P(t)'s exponentials in their shadow: each
+      // MFMA of the dependent chain is followed by two exponentials and the
+      // arithmetic around them
+      gemm0(snext);
+      const float ps = probs(scur, m, pb);
+      l += ps;
+      ovf |= !(ps < exp2f(kHeadroom));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // transcendental
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // other VALU
+      }
+      pp_barrier();
+      // I1: V(t) to registers, copy of K(t+4); K(t+2) complete after the wait
+      load_v(vslot(ic<TT>()));
+      dma_k(kslot(ic<TT>()), t + 4);
+      wait_vm<4>();
+      pp_barrier();
+      // I2: O += V(t)^T P(t); keys of S(t+1) past the end masked
+      gemm1(pb);
+      mask(snext, (t + 1) * kPK);
+      pp_barrier();
+      // I3: K(t+2) to registers, copy of V(t+3); V(t+1) complete after the wait
+      load_k(kslot(ic<TT + 2>()));
+      dma_v(vslot(ic<TT + 3>()), t + 3);
+      wait_vm<4>();
+      pp_barrier();
+    };
+    // The loops run a multiple of 4 iterations (the slots cycle with period
+    // 4 and the unrolled body has no exit in the middle, which keeps every
+    // value in one register assignment): iterations past the last tile copy
+    // zero rows and mask every key.  A wave without query rows (a sequence's
+    // last, partial query tile) only copies its share of every tile, with the
+    // same waits and barriers.
+    auto copy_only = [&](auto tt_c, int t) {
+      constexpr int TT = decltype(tt_c)::value;
+      pp_barrier();
+      dma_k(kslot(ic<TT>()), t + 4);
+      wait_vm<4>();
+      pp_barrier();
+      pp_barrier();
+      dma_v(vslot(ic<TT + 3>()), t + 3);
+      wait_vm<4>();
+      pp_barrier();
+    };
+    if (wave_rows) {
+      for (int t0 = 0; t0 < nT; t0 += 4) {
+        iter(ic<0>(), t0);
+        iter(ic<1>(), t0 + 1);
+        iter(ic<2>(), t0 + 2);
+        iter(ic<3>(), t0 + 3);
+      }
+    } else {
+      for (int t0 = 0; t0 < nT; t0 += 4) {
+        copy_only(ic<0>(), t0);
+        copy_only(ic<1>(), t0 + 1);
+        copy_only(ic<2>(), t0 + 2);
+        copy_only(ic<3>(), t0 + 3);
+      }
+    }
+    if (grp == 0) pp_barrier();
+    wait_vm<0>();  // no copy may land in LDS after the workgroup ends
+    if (ovf) ovf_any = 1;
+    __syncthreads();
+    if (ovf_any) {
+      // ---- slow pass (a later key outscored the first tile by kHeadroom):
+      // one tile at a time through slots Ka / Va, online softmax with a
+      // moving maximum and O rescaled when it moves
+      m = -INFINITY;
+      l = 0.0f;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+      for (int kt = 0; kt < nT; ++kt) {
+        dma_k(Ka, kt);
+        dma_v(Va, kt);
+        wait_vm<0>();
+        __syncthreads();
+        if (wave_rows) {
+          load_k(Ka);
+          load_v(Va);
+          f32x16 s;
+          gemm0(s);
+          mask(s, kt * kPK);
+          const float m_new = fmaxf(m, tile_max(s));
+          const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+          m = m_new;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+          bf16x8 pq[2];
+          l = l * alpha + probs(s, m, pq);
+          gemm1(pq);
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- epilogue: O = O^T / l
+  uint16_t *op = p.o + static_cast<int64_t>(q_begin) * p.o_tok + h * p.o_head;
+  const float lt = half_sum(l);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (row_q < Lq) {
+    uint16_t *orow = op + static_cast<int64_t>(row_q) * p.o_tok;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<__bf16>(o[db][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4 *>(orow + d) = v;
+      }
+  }
+}
+
 template <int D>
 static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   constexpr int BQ = 32 * kWaves;
@@ -524,6 +923,10 @@ static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   p.o_tok = a->o_tok_stride; p.o_head = a->o_head_stride;
   p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   if (p.n_wg == 0) return PKV_OK;
+  if (D == 128) {
+    hipLaunchKernelGGL(attn_pp_kernel, dim3(p.n_wg), dim3(kThreads), 0, st, p);
+    return check_launch("attn_pp_kernel");
+  }
   hipLaunchKernelGGL((attn_fwd_kernel<D>), dim3(p.n_wg), dim3(kThreads), 0, st, p);
   return check_launch("attn_fwd_kernel");
 }
