@@ -7,7 +7,11 @@ block -- is captured once with torch.cuda.graph and replayed.  Each replay
 starts from the same full cache state (pools, merge accumulators, state
 records, counters) and must reproduce the bytes of an eager run of the same
 step: pools, state records and counters bit-exact, every attention output
-equal to the eager kernel's.  Capture itself fails if any op synchronises
+equal to the eager kernel's.  The replayed state is also checked against
+the CPU oracle (oracle.MegaCacheRef driven with the same data): pools,
+counters and state records bit-exact, every replayed attention output within
+max-abs 2e-2 / mean-abs 2e-3 of float64 attention over the oracle's packed
+K / V.  Capture itself fails if any op synchronises
 with the host, so a passing capture shows the step is sync-free (the plan
 never leaves the device).  The replays are interleaved with eager work and
 synchronisations, and every replay is checked, not only the first.
@@ -22,7 +26,7 @@ import torch
 from oracle import oracle as O
 if torch.cuda.is_available():
     from gpu_util import DEV, to_dev
-    from test_gpu_megacache import _build
+    from test_gpu_megacache import _build, _compare_pools
 
 pytestmark = pytest.mark.gpu
 
@@ -48,7 +52,9 @@ def _restore(live, snap):
 
 
 def _rand(rng, *shape):
-    return to_dev(O.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))).view(torch.bfloat16)
+    """(host bf16 bits, device tensor) of the same N(0, 1) draw."""
+    host = O.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))
+    return host, to_dev(host).view(torch.bfloat16)
 
 
 def test_cache_step_graph_replays_match_eager():
@@ -59,15 +65,30 @@ def test_cache_step_graph_replays_match_eager():
     L, H, D, FS, W, F = 2, 6, 128, 448, 16, 3
     labels = [[-1, 1, 2, -1, 1, 2], [2, -1, 1, 1, 2, -1]]
     print("graph capture: L=2 H=6 D=128 FSEQ=448, noisy + clean step of 3 frames", flush=True)
-    caches, _, _ = _build(L, H, D, FS, W, labels, chunks=F)
+    caches, ref, _ = _build(L, H, D, FS, W, labels, chunks=F)
     # prefill 8 clean blocks so that every strategy has middle / merge content
     for b in range(8):
         for layer in range(L):
-            caches[layer].update(_rand(rng, 1, F * FS, H, D), _rand(rng, 1, F * FS, H, D), b * F * FS,
+            (kh, kd), (vh, vd) = _rand(rng, F * FS, H, D), _rand(rng, F * FS, H, D)
+            caches[layer].update(kd.view(1, F * FS, H, D), vd.view(1, F * FS, H, D), b * F * FS,
                                  cache_update_mode="clean")
+            ref.update(layer, kh, vh, b * F * FS, "clean")
     start = 8 * F * FS
-    ins = {(p, layer): (_rand(rng, 1, F * FS, H, D), _rand(rng, 1, F * FS, H, D), _rand(rng, 1, F * FS, H, D))
-           for p in ("noisy", "clean") for layer in range(L)}
+    host = {(p, layer): (_rand(rng, F * FS, H, D), _rand(rng, F * FS, H, D), _rand(rng, F * FS, H, D))
+            for p in ("noisy", "clean") for layer in range(L)}
+    ins = {key: tuple(d.view(1, F * FS, H, D) for _, d in val) for key, val in host.items()}
+
+    # the oracle's state after the step, and float64 attention on its packed K / V at each call
+    want_attn = []
+    cu_q = np.arange(0, F * FS + 1, FS)
+    for mode in ("noisy", "clean"):
+        for layer in range(L):
+            (kh, _), (vh, _), (qh, _) = host[(mode, layer)]
+            ref.update(layer, kh, vh, start, mode)
+            w = ref.plan_pack(layer, start, F)
+            want_attn.append(O.ragged_attention_ref(O.bf16_to_f32(qh).astype(np.float64), O.bf16_to_f32(w["k"]),
+                                                    O.bf16_to_f32(w["v"]), cu_q, w["cu"][:F * H + 1], heads_q=H,
+                                                    kv_per_head=True))
 
     def step():
         outs = []
@@ -115,3 +136,8 @@ def test_cache_step_graph_replays_match_eager():
             assert torch.equal(t, want[n]), f"replay {r}: {n} differs from the eager step"
         for i, (g, w) in enumerate(zip(g_outs, want_out)):
             assert torch.equal(g, w), f"replay {r}: attention output {i} differs from the eager step"
+        # against the oracle
+        _compare_pools(caches, ref, f"replay {r}")
+        for i, (g, w) in enumerate(zip(g_outs, want_attn)):
+            err = np.abs(g[0].float().cpu().numpy().astype(np.float64) - w)
+            assert err.max() < 2e-2 and err.mean() < 2e-3, f"replay {r}: attention {i} vs float64 {err.max()}"
