@@ -137,7 +137,8 @@ typedef struct pkv_merge_layer {
   int32_t *accum_group_ids;           /* [H,MMA,FSEQ] */
   float *accum_tokens_per_group;      /* [H,MMA,MTPA] */
   int32_t *accum_num_groups;          /* [H,MMA] */
-  float *accum_weight_sum;            /* [H,MMA] running sum of frame weights; NULL ok when weights == NULL */
+  float *accum_weight_sum;            /* [H,MMA] running sum of the block's frame weights (1 per
+                                         unweighted frame); NULL ok when weights == NULL */
   uint16_t *merge_k, *merge_v;        /* [H,MMB,MTPA,D] */
   int64_t *merge_pos;                 /* [H,MMB,MTPA,3] */
   int32_t *merge_token_count;         /* [H,MMB] */
@@ -328,7 +329,10 @@ int pkv_ragged_attn_fwd(const pkv_attn_args *args, pkv_stream_t stream);
 
 /* Bytes of device workspace pkv_cache_update needs for F frames per block.
  * The workspace starts with the 8 state-machine descriptor arrays of the
- * last call (pkv_state_desc order, each [H*F] int32, 256-byte aligned). */
+ * last call (pkv_state_desc order, each [H*F] int32, 256-byte aligned),
+ * followed by H int32 arrival counters.  The counters must be zero before the
+ * first call (allocate the workspace zero-filled); every call leaves them
+ * zero.  Calls that share one workspace must be ordered (one stream). */
 int64_t pkv_cache_update_workspace_size(const pkv_geometry *geo, int32_t frames);
 
 typedef struct pkv_update_args {
@@ -338,7 +342,7 @@ typedef struct pkv_update_args {
   int32_t pass_kind;         /* 0 noisy, 1 clean */
   int32_t shift_pending;     /* 1: this block's recent shift is already in the pool */
   int32_t spatial_width;     /* W of the (y, x) = (tok / W, tok % W) grid */
-  int32_t has_merge_head;    /* run the merge accumulator launch */
+  int32_t has_merge_head;    /* the layer has a Veil head: clean passes accumulate merges */
   const uint16_t *new_k;     /* [L_in, H, D] rows, token stride tok_stride */
   const uint16_t *new_v;
   int64_t tok_stride;        /* elements between consecutive tokens (H*D) */
@@ -349,6 +353,11 @@ typedef struct pkv_update_args {
   void *workspace;           /* pkv_cache_update_workspace_size bytes */
 } pkv_update_args;
 
+/* MegaCache.update of one layer (_mega_cache.py:136-414) in one launch:
+ * sink / recent routing of the F new frames with the recent FIFO shift, the
+ * state machine and middle-pool writes of a clean pass, the Veil merge
+ * accumulate (the pkv_merge_accum semantics, unweighted) and the counter
+ * commit.  Positions are the grid (t0 + f, tok / W, tok % W). */
 int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools,
                      const pkv_update_args *args, pkv_stream_t stream);
 

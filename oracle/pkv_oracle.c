@@ -438,7 +438,9 @@ void orc_update_frames(const uint16_t *new_k, const uint16_t *new_v, const int64
  * each head and dim the tokens in ascending order with one fp32 add into
  * the token's group accumulator (:193-209).  weights (nullable [F]) scale
  * each frame's contribution and turn the divisor into count * sum(w); the
- * reference operation is weights == NULL.  The finalize uses the IEEE
+ * reference operation is weights == NULL.  awsum (nullable) keeps the running
+ * sum of the block's frame weights, 1 per frame without weights, so that
+ * weighted and unweighted calls can continue each other's blocks.  The finalize uses the IEEE
  * reciprocal 1/div (the reference's --use_fast_math reciprocal is
  * approximate; 1/16 is exact either way). */
 void orc_merge_accum(const uint8_t *states, int H, int F, int FSEQ, int D, int MMA, int MMB, int MTPA,
@@ -506,7 +508,7 @@ void orc_merge_accum(const uint8_t *states, int H, int F, int FSEQ, int D, int M
               sum_v[(hs * MTPA + gid) * D + d] += vf;
             }
           }
-        if (weights && awsum) awsum[hs] += w;
+        if (awsum) awsum[hs] += w;
       }
       if (fin >= 0) { /* :215-249 */
         const int32_t ng = ang[hs];

@@ -13,6 +13,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "pkv_common.h"
@@ -134,273 +135,7 @@ __global__ void copy_frames_kernel(FrameSrc src, const int64_t *new_pos, PoolPtr
   }
 }
 
-// ---------------------------------------------------------------------------
-// fused MegaCache.update
-// ---------------------------------------------------------------------------
-// Per-head routing record produced by route_kernel and consumed by
-// scatter_kernel.
-struct Route {
-  int32_t sink_writes;   // frames 0..sink_writes-1 go to sink slots sink_first..
-  int32_t sink_first;
-  int32_t recent_first;  // frame sink_writes+i goes to recent slot recent_first+i
-  int32_t shift;         // move recent slot j+shift -> j for j < keep (0: none)
-  int32_t keep;
-  int32_t pad[3];
-};
-
-struct Workspace {
-  int32_t *desc[8];  // [H*F] each: the pkv_state_desc arrays
-  Route *route;      // [H]
-};
-
 __host__ __device__ inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
-
-__host__ __device__ inline Workspace carve_workspace(void *base, int H, int F) {
-  Workspace w;
-  char *p = static_cast<char *>(base);
-  const int64_t dbytes = align_up(static_cast<int64_t>(H) * F * 4, 256);
-  for (int i = 0; i < 8; ++i) w.desc[i] = reinterpret_cast<int32_t *>(p + i * dbytes);
-  w.route = reinterpret_cast<Route *>(p + 8 * dbytes);
-  return w;
-}
-
-// One thread per head: restore the committed counters, route the F new
-// frames between sink and recent (_mega_cache.py:226-323), advance the
-// state machine on clean passes (_mega_cache.py:329-347) and commit the
-// counters (_mega_cache.py:406-414).  The recent FIFO's shift-left is
-// applied once per block: noisy passes of a block and its clean pass all
-// restore the same committed state, shift by the same amount and overwrite
-// the same tail slots, so a pass that finds the shift already applied
-// (shift_pending) only rewrites the tail.  That reproduces the reference's
-// snapshot-and-restore contents without copying the recent pool.
-// A workgroup covers kRouteHeads heads; their state records are copied into
-// LDS with coalesced 4-byte accesses, updated there by one thread per head,
-// and copied back.
-constexpr int kRouteHeads = 64;
-constexpr int kRouteThreads = 256;
-__device__ void route_head(HeadState &s, int h, int F, int64_t t0, int pass_kind, int shift_pending, int max_sink,
-                           int max_recent, const int64_t *sink_caps, int64_t *committed_vc, int64_t *vc,
-                           const Workspace &ws);
-
-__global__ void __launch_bounds__(kRouteThreads) route_kernel(HeadState *states, int H, int F, int64_t t0,
-                                                              int pass_kind, int shift_pending, int max_sink,
-                                                              int max_recent, const int64_t *sink_caps,
-                                                              int64_t *committed_vc, int64_t *vc, Workspace ws) {
-  __shared__ __attribute__((aligned(16))) HeadState s_st[kRouteHeads];
-  const int h0 = blockIdx.x * kRouteHeads;
-  const int nh = min(kRouteHeads, H - h0);
-  const int words = nh * static_cast<int>(sizeof(HeadState)) / 8;
-  uint2 *g = reinterpret_cast<uint2 *>(states + h0);
-  uint2 *l = reinterpret_cast<uint2 *>(s_st);
-  stage_words(l, g, words);
-  __syncthreads();
-  if (static_cast<int>(threadIdx.x) < nh)
-    route_head(s_st[threadIdx.x], h0 + threadIdx.x, F, t0, pass_kind, shift_pending, max_sink, max_recent, sink_caps,
-               committed_vc, vc, ws);
-  __syncthreads();
-  if (pass_kind == 1)
-    for (int i = threadIdx.x; i < words; i += blockDim.x) g[i] = l[i];
-}
-
-__device__ void route_head(HeadState &s, int h, int F, int64_t t0, int pass_kind, int shift_pending, int max_sink,
-                           int max_recent, const int64_t *sink_caps, int64_t *committed_vc, int64_t *vc,
-                           const Workspace &ws) {
-  const int64_t sc = committed_vc[h * 3 + 0];
-  const int64_t mc = committed_vc[h * 3 + 1];
-  const int64_t rc = committed_vc[h * 3 + 2];
-  int64_t cap = sink_caps[h];
-  if (cap > max_sink) cap = max_sink;
-  int64_t sw = cap - sc;
-  if (sw > F) sw = F;
-  if (sw < 0) sw = 0;
-  const int64_t rw = F - sw;
-  Route r;
-  r.sink_writes = static_cast<int32_t>(sw);
-  r.sink_first = static_cast<int32_t>(sc);
-  r.shift = 0;
-  r.keep = 0;
-  int64_t rc_post = rc;
-  if (rw > 0) {
-    const int64_t total = rc + rw;
-    if (total <= max_recent) {
-      r.recent_first = static_cast<int32_t>(rc);
-      rc_post = total;
-    } else {
-      const int64_t evict = total - max_recent;
-      if (!shift_pending) {
-        r.shift = static_cast<int32_t>(evict);
-        r.keep = static_cast<int32_t>(max_recent - evict);
-      }
-      r.recent_first = static_cast<int32_t>(max_recent - rw);
-      rc_post = max_recent;
-    }
-  } else {
-    r.recent_first = static_cast<int32_t>(rc);
-  }
-  ws.route[h] = r;
-  vc[h * 3 + 0] = sc + sw;
-  vc[h * 3 + 1] = mc;
-  vc[h * 3 + 2] = rc_post;
-
-  pkv_state_desc out;
-  out.dst_kind = ws.desc[0];
-  out.dst_slot = ws.desc[1];
-  out.src_frame = ws.desc[2];
-  out.src_head = ws.desc[3];
-  out.merge_accum_slot = ws.desc[4];
-  out.merge_local_idx = ws.desc[5];
-  out.merge_finalize_completed_idx = ws.desc[6];
-  out.merge_is_new_block = ws.desc[7];
-  for (int f = 0; f < F; ++f) {
-    FrameDesc d = skip_desc();
-    if (pass_kind == 1) d = sm_step(s, static_cast<int32_t>(t0 + f));
-    store_desc(out, h * F + f, f, h, d);
-  }
-  if (pass_kind == 1) {
-    committed_vc[h * 3 + 0] = sc + sw;
-    committed_vc[h * 3 + 1] = mc;
-    committed_vc[h * 3 + 2] = rc_post;
-  }
-}
-
-// grid = (ceil(FSEQ / kScatTok), H), one thread per (token, 16-byte chunk).
-// Each thread first loads everything it will write (the recent slots the
-// FIFO shift moves and every new frame), then stores: the shift into
-// ascending slots, the new frames into their sink / recent slots and, for
-// middle descriptors, into their middle slots.  Loading before storing keeps
-// several 16-byte reads in flight per thread and makes the in-place shift
-// safe whatever slots the new frames land in.
-constexpr int kScatTok = 16;
-constexpr int kScatBatch = 4;  // frames (and shifted slots) staged per batch
-struct ScatterArgs {
-  FrameSrc src;
-  PosSrc pos;
-  PoolPtrs pools;
-  Workspace ws;
-  int layer, H, F, FSEQ, D, max_sink, max_middle, max_recent;
-};
-
-// tile bx of head h (kScatTok tokens)
-__device__ void scatter_body(const ScatterArgs &sa, int bx, int h) {
-  const FrameSrc &src = sa.src;
-  const PosSrc &pos = sa.pos;
-  const PoolPtrs &pools = sa.pools;
-  const Workspace &ws = sa.ws;
-  const int layer = sa.layer, H = sa.H, F = sa.F, FSEQ = sa.FSEQ, D = sa.D;
-  const int max_sink = sa.max_sink, max_middle = sa.max_middle, max_recent = sa.max_recent;
-  const Route r = ws.route[h];
-  const int tok0 = bx * kScatTok;
-  const int cpt = D / 8;
-  const int64_t lh = static_cast<int64_t>(layer) * H + h;
-  const int64_t slot_elems = static_cast<int64_t>(FSEQ) * D;
-  uint16_t *sink_k = pools.k[0] + lh * max_sink * slot_elems;
-  uint16_t *sink_v = pools.v[0] + lh * max_sink * slot_elems;
-  uint16_t *mid_k = pools.k[1] + lh * max_middle * slot_elems;
-  uint16_t *mid_v = pools.v[1] + lh * max_middle * slot_elems;
-  uint16_t *rec_k = pools.k[2] + lh * max_recent * slot_elems;
-  uint16_t *rec_v = pools.v[2] + lh * max_recent * slot_elems;
-  const int32_t *dkind = ws.desc[0];
-  const int32_t *dslot = ws.desc[1];
-
-  for (int i = threadIdx.x; i < kScatTok * cpt; i += blockDim.x) {
-    const int tok = tok0 + i / cpt, c = (i % cpt) * 8;
-    if (tok >= FSEQ) break;
-    const int64_t e = static_cast<int64_t>(tok) * D + c;
-    uint4 kk[kScatBatch], vv[kScatBatch];
-    // recent FIFO shift: slot j <- slot j + shift for j < keep (all sources
-    // of a batch read before its stores; batches ascend, and a slot written
-    // by one batch is never a source of a later batch since sources are
-    // >= shift > destinations of earlier batches)
-    for (int j0 = 0; j0 < r.keep; j0 += kScatBatch) {
-      const int n = min(kScatBatch, r.keep - j0);
-#pragma unroll
-      for (int b = 0; b < kScatBatch; ++b)
-        if (b < n) {
-          kk[b] = ld16(rec_k + (j0 + b + r.shift) * slot_elems + e);
-          vv[b] = ld16(rec_v + (j0 + b + r.shift) * slot_elems + e);
-        }
-#pragma unroll
-      for (int b = 0; b < kScatBatch; ++b)
-        if (b < n) {
-          st16(rec_k + (j0 + b) * slot_elems + e, kk[b]);
-          st16(rec_v + (j0 + b) * slot_elems + e, vv[b]);
-        }
-    }
-    for (int f0 = 0; f0 < F; f0 += kScatBatch) {
-      const int n = min(kScatBatch, F - f0);
-#pragma unroll
-      for (int b = 0; b < kScatBatch; ++b)
-        if (b < n) {
-          const int64_t so = src.off(f0 + b, h, tok) + c;
-          kk[b] = ld16(src.k + so);
-          vv[b] = ld16(src.v + so);
-        }
-#pragma unroll
-      for (int b = 0; b < kScatBatch; ++b) {
-        if (b >= n) continue;
-        const int f = f0 + b;
-        if (f < r.sink_writes) {
-          const int64_t s = r.sink_first + f;
-          st16(sink_k + s * slot_elems + e, kk[b]);
-          st16(sink_v + s * slot_elems + e, vv[b]);
-        } else {
-          const int64_t s = r.recent_first + (f - r.sink_writes);
-          st16(rec_k + s * slot_elems + e, kk[b]);
-          st16(rec_v + s * slot_elems + e, vv[b]);
-        }
-        if (dkind[h * F + f] == PKV_DST_MIDDLE) {
-          const int64_t s = dslot[h * F + f];
-          if (s >= 0 && s < max_middle) {
-            st16(mid_k + s * slot_elems + e, kk[b]);
-            st16(mid_v + s * slot_elems + e, vv[b]);
-          }
-        }
-      }
-    }
-  }
-
-  // positions: one thread per token of the tile
-  const int t = threadIdx.x;
-  if (t < kScatTok && tok0 + t < FSEQ) {
-    const int tok = tok0 + t;
-    const int64_t pe = static_cast<int64_t>(tok) * 3;
-    const int64_t pslot = static_cast<int64_t>(FSEQ) * 3;
-    int64_t *sink_p = pools.pos[0] + lh * max_sink * pslot;
-    int64_t *mid_p = pools.pos[1] + lh * max_middle * pslot;
-    int64_t *rec_p = pools.pos[2] + lh * max_recent * pslot;
-    for (int j = 0; j < r.keep; ++j) {
-      const int64_t *sp = rec_p + (j + r.shift) * pslot + pe;
-      const int64_t a = sp[0], b = sp[1], cc = sp[2];
-      int64_t *dp = rec_p + j * pslot + pe;
-      dp[0] = a;
-      dp[1] = b;
-      dp[2] = cc;
-    }
-    for (int f = 0; f < F; ++f) {
-      int64_t pt, py, px;
-      pos.get(f, h, tok, pt, py, px);
-      int64_t *dp;
-      if (f < r.sink_writes)
-        dp = sink_p + (r.sink_first + f) * pslot + pe;
-      else
-        dp = rec_p + (r.recent_first + (f - r.sink_writes)) * pslot + pe;
-      dp[0] = pt;
-      dp[1] = py;
-      dp[2] = px;
-      if (dkind[h * F + f] == PKV_DST_MIDDLE) {
-        const int64_t s = dslot[h * F + f];
-        if (s >= 0 && s < max_middle) {
-          int64_t *mp = mid_p + s * pslot + pe;
-          mp[0] = pt;
-          mp[1] = py;
-          mp[2] = px;
-        }
-      }
-    }
-  }
-}
-
-__global__ void __launch_bounds__(256) scatter_kernel(ScatterArgs sa) { scatter_body(sa, blockIdx.x, blockIdx.y); }
 
 // ---------------------------------------------------------------------------
 // Veil merge accumulator (mega_merge_accum.cu:52-252)
@@ -738,8 +473,8 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
       a.ws.ng[di] = ng;
       a.ws.width[di] = list_w;
       float ws = 1.0f;
-      if (a.weights && a.ml.accum_weight_sum) {
-        ws = s_wsum[slot] + a.weights[f];
+      if (a.ml.accum_weight_sum) {
+        ws = s_wsum[slot] + (a.weights ? a.weights[f] : 1.0f);
         s_wsum[slot] = ws;
         a.ml.accum_weight_sum[hs] = ws;
       }
@@ -763,21 +498,6 @@ __device__ void merge_prep_body(const MergeArgs &a, int h, int32_t *smem) {
 __global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) {
   extern __shared__ int32_t smem[];
   merge_prep_body(a, blockIdx.x, smem);
-}
-
-// The scatter of one update (blocks [0, n_scatter), gx tiles per head) and
-// its merge preparation (the next H blocks) touch disjoint memory, so they
-// share one launch and overlap: the latency-bound per-head merge work runs
-// beside the bandwidth-bound scatter.
-static_assert(kMergeThreads == 256, "scatter and merge prep share the block size");
-__global__ void __launch_bounds__(256) scatter_merge_prep_kernel(ScatterArgs sa, MergeArgs ma, int gx,
-                                                                  int n_scatter) {
-  extern __shared__ int32_t smem[];
-  const int b = blockIdx.x;
-  if (b < n_scatter)
-    scatter_body(sa, b % gx, b / gx);
-  else
-    merge_prep_body(ma, b - n_scatter, smem);
 }
 
 // Workgroup = (range of kGroupsPerWg groups, head); thread = (group, 8-wide
@@ -1056,6 +776,618 @@ static int launch_merge(const MergeArgs &ma, hipStream_t st) {
   return launch_merge_accum(ma, st);
 }
 
+// ---------------------------------------------------------------------------
+// fused MegaCache.update (_mega_cache.py:136-414): one launch per call
+// ---------------------------------------------------------------------------
+// The grid holds, for every head, n_merge merge tiles (the Veil accumulate
+// of a clean pass in a layer with a Veil head; they come first in the grid
+// so that their longer dependency chains start early) and n_scat token
+// tiles (the new frames routed to sink / recent slots, the recent FIFO
+// shift, the middle-pool writes and the positions).
+//
+// Every workgroup of head h stages h's state record and committed counters
+// and routes the frames itself (_mega_cache.py:226-323).  The workgroups
+// that need descriptors -- token tiles of Wave / Anchor / lag heads for the
+// middle slots, merge tiles of Veil heads -- also run the state machine over
+// the call's frames (_mega_cache.py:329-347) on their LDS copy of the
+// record.  The inputs are the same for all of them, so all derive the same
+// routing and descriptors.  No workgroup writes what another one reads: the
+// workgroup that arrives last at the head's counter arrive[h] (zero between
+// calls; that workgroup resets it) writes the advanced record, the counters
+// (_mega_cache.py:406-414), the descriptors and the merge bookkeeping that
+// every merge tile of the head reads (group ids, group count, weight sum).
+// Each workgroup increments the counter only after a barrier that follows
+// its last read of that shared data.
+//
+// The recent FIFO shift-left is applied once per block: noisy passes of a
+// block and its clean pass all restore the same committed counters, shift
+// by the same amount and overwrite the same tail slots, so a pass that
+// finds the shift already applied (shift_pending) only rewrites the tail.
+// That reproduces the reference's snapshot-and-restore contents without
+// copying the recent pool.
+constexpr int kUpdThreads = 256;
+constexpr int kUpdMaxFrames = 64;
+constexpr int kScatBatch = 4;   // new frames loaded per batch
+constexpr int kShiftBatch = 2;  // shifted recent slots loaded per batch
+constexpr int kUpdAccBatch = 4; // member tokens loaded per batch by a merge tile
+constexpr int kStateWords = static_cast<int>(sizeof(HeadState) / 4);
+constexpr int kArriveFan = 8;      // arrival sub-counters per head
+constexpr int kArriveStride = 32;  // int32 words between counters (128 bytes)
+
+// 16-byte access at a 32-bit byte offset from a workgroup-uniform base: the
+// base stays in scalar registers and the address costs one vector register
+__device__ inline uint4 ld16o(const void *base, uint32_t off) {
+  return *reinterpret_cast<const uint4 *>(static_cast<const char *>(base) + off);
+}
+__device__ inline void st16o(void *base, uint32_t off, uint4 v) {
+  *reinterpret_cast<uint4 *>(static_cast<char *>(base) + off) = v;
+}
+static_assert(kStateWords <= kUpdThreads, "one state word per thread");
+
+// list sources of a merge frame's groups
+constexpr int kSrcNone = -2;  // not a merge frame (slot untouched)
+constexpr int kSrcGrid = -1;  // the call's arithmetic grid (block began in this call)
+                              // s >= 0: the group ids stored for slot s
+
+struct Route {
+  int64_t vc_post[3];    // counters after the call
+  int32_t sink_writes;   // frames 0..sink_writes-1 go to sink slots sink_first..
+  int32_t sink_first;
+  int32_t recent_first;  // frame sink_writes+i goes to recent slot recent_first+i
+  int32_t shift;         // move recent slot j+shift -> j for j < keep (0: none)
+  int32_t keep;
+};
+
+// _mega_cache.py:226-323 for one head: frames fill the sink up to the
+// head's cap, the rest enter the recent FIFO, evicting from its front when
+// it is full
+__device__ inline Route route_frames(int64_t sc, int64_t mc, int64_t rc, int64_t cap, int F, int max_sink,
+                                     int max_recent, int shift_pending) {
+  // counters outside their pools (only a corrupted record holds them) are
+  // clamped so that every write stays inside the head's slots
+  sc = sc < 0 ? 0 : sc;
+  rc = rc < 0 ? 0 : (rc > max_recent ? max_recent : rc);
+  if (cap > max_sink) cap = max_sink;
+  int64_t sw = cap - sc;
+  if (sw > F) sw = F;
+  if (sw < 0) sw = 0;
+  const int64_t rw = F - sw;
+  Route r;
+  r.sink_writes = static_cast<int32_t>(sw);
+  r.sink_first = static_cast<int32_t>(sc);
+  r.recent_first = static_cast<int32_t>(rc);
+  r.shift = 0;
+  r.keep = 0;
+  int64_t rc_post = rc;
+  if (rw > 0) {
+    const int64_t total = rc + rw;
+    if (total <= max_recent) {
+      rc_post = total;
+    } else {
+      const int64_t evict = total - max_recent;
+      if (!shift_pending) {
+        r.shift = static_cast<int32_t>(evict);
+        r.keep = static_cast<int32_t>(max_recent - evict);
+      }
+      r.recent_first = static_cast<int32_t>(max_recent - rw);
+      rc_post = max_recent;
+    }
+  }
+  r.vc_post[0] = sc + sw;
+  r.vc_post[1] = mc;
+  r.vc_post[2] = rc_post;
+  return r;
+}
+
+struct UpdArgs {
+  HeadState *states;
+  const int64_t *sink_caps;
+  int64_t *committed_vc, *vc;
+  FrameSrc src;
+  PoolPtrs pools;
+  pkv_merge_layer ml;  // this layer's merge pools
+  pkv_state_desc desc;
+  int32_t *arrive;     // [H]
+  // byte strides of the new frames (frame, head, token); every offset into
+  // them and into one head's pools is below 2^31
+  uint32_t src_fb, src_hb, src_tb;
+  int64_t t0;
+  int layer, H, F, FSEQ, D, width, max_sink, max_middle, max_recent, MMA, MMB, MTPA;
+  int pass_kind, shift_pending, n_merge, n_scat;
+};
+
+struct UpdShared {
+  HeadState st;
+  FrameDesc desc[kUpdMaxFrames];
+  Route r;
+  int32_t staged, machine_done, last;
+  // merge bookkeeping: per frame, the list source and group count of its
+  // block; per slot, the source, group count and weight sum after the call
+  // and the stored-id check (-1 not done, 0 not the regular grid, else its
+  // width); the call's grid: group count, columns, regular width (0: none)
+  int32_t f_src[kUpdMaxFrames];
+  int32_t f_ng[kUpdMaxFrames];
+  int64_t f_tpos[kUpdMaxFrames];
+  int32_t s_src[kMaxMergeSlots];
+  int32_t s_ng[kMaxMergeSlots];
+  int64_t s_tpos[kMaxMergeSlots];
+  float s_wsum[kMaxMergeSlots];
+  int32_t s_grid[kMaxMergeSlots];
+  int32_t grid_ng, grid_cols, grid_w;
+};
+
+// group of token t on the arithmetic grid (y = t / W, x = t % W) in patches
+// of p (mega_merge_accum.cu:100-184, ids past the group count fold into 0)
+__device__ inline int32_t grid_gid(int t, int W, int p, int cols, int ng) {
+  const int32_t y = t / W, x = t % W;
+  const int32_t g = (p > 0 ? y / p : 0) * cols + (p > 0 ? x / p : 0);
+  return (g < 0 || g >= ng) ? 0 : g;
+}
+
+// thread 0: descriptors of the call's frames on the LDS record
+// (anchor_store_update.cu:257-269; noisy passes emit SKIP)
+__device__ void upd_machine(const UpdArgs &a, UpdShared &sh) {
+  for (int f = 0; f < a.F; ++f)
+    sh.desc[f] = a.pass_kind == 1 ? sm_step(sh.st, static_cast<int32_t>(a.t0 + f)) : skip_desc();
+  sh.machine_done = 1;
+}
+
+// thread 0, after upd_machine on a Veil head: where each merge frame's
+// group lists come from, and every touched slot's group count and running
+// weight sum (one per frame: cache updates are unweighted)
+__device__ void upd_merge_plan(const UpdArgs &a, int h, UpdShared &sh) {
+  const int p = sh.st.patch_size, FSEQ = a.FSEQ, W = a.width, MTPA = a.MTPA;
+  const int maxx = min(W, FSEQ) - 1, maxy = (FSEQ - 1) / W;
+  const int cols = p > 0 ? maxx / p + 1 : 1, rows = p > 0 ? maxy / p + 1 : 1;
+  const int we = maxx + 1;
+  sh.grid_cols = cols;
+  sh.grid_ng = min(rows * cols, MTPA);
+  sh.grid_w = (p > 0 && FSEQ % we == 0 && we % p == 0 && (FSEQ / we) % p == 0 && rows * cols <= MTPA) ? we : 0;
+  for (int s = 0; s < a.MMA; ++s) {
+    sh.s_src[s] = kSrcNone;
+    sh.s_grid[s] = -1;
+  }
+  for (int f = 0; f < a.F; ++f) {
+    const FrameDesc d = sh.desc[f];
+    sh.f_src[f] = kSrcNone;
+    if (d.kind != PKV_DST_MERGE_ACCUM || d.accum_slot < 0 || d.accum_slot >= a.MMA) continue;
+    const int s = d.accum_slot;
+    const int64_t hs = static_cast<int64_t>(h) * a.MMA + s;
+    if (d.is_new_block) {
+      sh.s_src[s] = kSrcGrid;
+      sh.s_ng[s] = sh.grid_ng;
+      sh.s_tpos[s] = a.t0 + f;
+      sh.s_wsum[s] = 0.0f;
+    } else if (sh.s_src[s] == kSrcNone) {
+      sh.s_src[s] = s;
+      sh.s_ng[s] = min(a.ml.accum_num_groups[hs], MTPA);
+      sh.s_tpos[s] = 0;
+      sh.s_wsum[s] = a.ml.accum_weight_sum ? a.ml.accum_weight_sum[hs] : 0.0f;
+    }
+    sh.s_wsum[s] += 1.0f;
+    sh.f_src[f] = sh.s_src[s];
+    sh.f_ng[f] = sh.s_ng[s];
+    sh.f_tpos[f] = sh.s_tpos[s];
+  }
+}
+
+// Width W of the regular patch grid when the group ids stored for a block
+// are exactly its ids (group of token t = ((t / W) / p) * (W / p) +
+// (t % W) / p), else 0; the same in every thread (a block-wide vote).
+__device__ int stored_grid_width(const int32_t *gids, int FSEQ, int W, int p, int ng) {
+  const bool ok = W > 0 && p > 0 && FSEQ % W == 0 && W % p == 0 && (FSEQ / W) % p == 0 && ng == FSEQ / (p * p);
+  bool bad = false;
+  if (ok) {
+    const int cols = W / p;
+    for (int t = threadIdx.x; t < FSEQ; t += blockDim.x) bad |= gids[t] != ((t / W) / p) * cols + (t % W) / p;
+  }
+  const int any_bad = __syncthreads_or(bad);
+  return ok && !any_bad ? W : 0;
+}
+
+// LDS words of a merge tile's lists: local ids and members [FSEQ] each,
+// starts [gpt + 2], per-wave counts [kMergeWaves * (gpt + 1)], scan partials
+__host__ __device__ inline int64_t tile_list_words(int FSEQ, int gpt) {
+  return 2 * static_cast<int64_t>(FSEQ) + (gpt + 2) + kMergeWaves * static_cast<int64_t>(gpt + 1) + kUpdThreads;
+}
+
+// Member lists of groups [g0, g0 + gpt) in ascending token order (the
+// reference's accumulation order) from the call's grid ids (src ==
+// kSrcGrid) or the ids stored for slot src: a stable CSR over gpt + 1 local
+// groups, the last one collecting every other token.
+__device__ void tile_lists(const UpdArgs &a, const UpdShared &sh, int src, int h, int g0, int gpt, int32_t *dyn) {
+  int32_t *lid = dyn, *members = lid + a.FSEQ, *gstart = members + a.FSEQ;
+  int32_t *cntw = gstart + gpt + 2, *part = cntw + kMergeWaves * (gpt + 1);
+  const int p = sh.st.patch_size;
+  const int32_t *stored =
+      src >= 0 ? a.ml.accum_group_ids + (static_cast<int64_t>(h) * a.MMA + src) * a.FSEQ : nullptr;
+  __syncthreads();  // readers of the previous lists are done
+  for (int t = threadIdx.x; t < a.FSEQ; t += blockDim.x) {
+    const int g = stored ? stored[t] : grid_gid(t, a.width, p, sh.grid_cols, sh.grid_ng);
+    const int l = g - g0;
+    lid[t] = (l >= 0 && l < gpt) ? l : gpt;
+  }
+  __syncthreads();
+  build_csr(lid, a.FSEQ, gpt + 1, cntw, gstart, members, part);
+}
+
+// Merge tile mt of head h: groups [mt * gpt, (mt + 1) * gpt), thread =
+// (group, 8-wide dim chunk), every accumulator element owned by one thread
+// for all frames (mega_merge_accum.cu:52-252).  Per frame in order: a slot
+// switch stores / loads the accumulators, a new block zeroes them and its
+// owner threads write the group's token count and position, the members are
+// added in ascending token order (one fp32 add each), and a finalize writes
+// bf16(sum * (1 / (count * block_frames))) and the anchor position.
+// Groups per merge tile: each wave covers 64 / (D / 8) groups of K (even
+// waves) or V (odd waves), the wave pairs side by side
+__host__ __device__ inline int merge_tile_groups(int D) { return (kUpdThreads / 128) * (64 / (D / 8)); }
+
+__device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, int32_t *dyn) {
+  const int tid = threadIdx.x, D = a.D, MTPA = a.MTPA, FSEQ = a.FSEQ;
+  const int cpt = D / 8, gpw = 64 / cpt, gpt = merge_tile_groups(D);
+  const int wave = tid >> 6, lane = tid & 63;
+  const int is_v = wave & 1;  // wave-uniform: K or V
+  const int gl = (wave >> 1) * gpw + lane / cpt, c = (lane % cpt) * 8;
+  const int g = mt * gpt + gl;
+  const bool own = lane / cpt < gpw && g < MTPA;
+  const bool meta = own && !is_v && c == 0;  // writes the group's count and positions
+  const int32_t p = sh.st.patch_size, bf = sh.st.block_frames;
+  const pkv_merge_layer &ml = a.ml;
+  const uint16_t *src = is_v ? a.src.v : a.src.k;
+  float *acc_sum = is_v ? ml.accum_sum_v : ml.accum_sum_k;
+  uint16_t *merge_out = is_v ? ml.merge_v : ml.merge_k;
+  const int32_t *members = dyn + FSEQ, *gstart = members + FSEQ;
+  float ax[8];
+  int cur = -1;
+  int list_src = kSrcNone;  // source of the CSR lists in LDS
+  auto store_acc = [&](int slot) {
+    const int64_t o = ((static_cast<int64_t>(h) * a.MMA + slot) * MTPA + g) * D + c;
+    for (int e = 0; e < 8; ++e) acc_sum[o + e] = ax[e];
+  };
+  for (int f = 0; f < a.F; ++f) {
+    const int src_kind = sh.f_src[f];
+    if (src_kind == kSrcNone) continue;
+    const uint32_t fo = f * a.src_fb + h * a.src_hb + c * 2;
+    const FrameDesc d = sh.desc[f];
+    const int slot = d.accum_slot, is_new = d.is_new_block, fin = d.finalize_idx;
+    const int ng = sh.f_ng[f];
+    const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
+    // the block's lists: closed form on a regular grid of width W, else CSR
+    int W;
+    if (src_kind == kSrcGrid) {
+      W = sh.grid_w;
+    } else {
+      if (sh.s_grid[src_kind] < 0)
+        sh.s_grid[src_kind] = stored_grid_width(ml.accum_group_ids + hs * FSEQ, FSEQ, min(a.width, FSEQ), p, ng);
+      W = sh.s_grid[src_kind];
+    }
+    if (W == 0 && list_src != src_kind) {
+      tile_lists(a, sh, src_kind, h, mt * gpt, gpt, dyn);
+      list_src = src_kind;
+    }
+    if (own) {
+      const int cnt = W ? p * p : gstart[gl + 1] - gstart[gl];
+      if (is_new && meta) {
+        ml.accum_tokens_per_group[hs * MTPA + g] = g < ng ? static_cast<float>(cnt) * static_cast<float>(bf) : 0.0f;
+        if (g < ng) {
+          int64_t *ap = ml.accum_pos + (hs * MTPA + g) * 3;
+          ap[0] = sh.f_tpos[f];
+          ap[1] = (g / sh.grid_cols) * p;
+          ap[2] = (g % sh.grid_cols) * p;
+        }
+      }
+      if (slot != cur) {
+        if (cur >= 0) store_acc(cur);
+        cur = slot;
+        if (!is_new) {
+          const int64_t o = (hs * MTPA + g) * D + c;
+          for (int e = 0; e < 8; ++e) ax[e] = acc_sum[o + e];
+        }
+      }
+      if (is_new)
+        for (int e = 0; e < 8; ++e) ax[e] = 0.0f;
+      if (g < ng) {
+        const int gcols = W ? W / p : 1;
+        const int gbase = W ? (g / gcols) * p * W + (g % gcols) * p : 0;
+        const int m0 = W ? 0 : gstart[gl], m1 = W ? p * p : gstart[gl + 1];
+        for (int mb = m0; mb < m1; mb += kUpdAccBatch) {
+          const int n = min(kUpdAccBatch, m1 - mb);
+          uint4 xx[kUpdAccBatch];
+#pragma unroll
+          for (int b = 0; b < kUpdAccBatch; ++b)
+            if (b < n) {
+              const int m = mb + b;
+              const int tok = W ? gbase + (m / p) * W + m % p : members[m];
+              xx[b] = ld16o(src, fo + tok * a.src_tb);
+            }
+#pragma unroll
+          for (int b = 0; b < kUpdAccBatch; ++b)
+            if (b < n) {
+              const uint32_t xw[4] = {xx[b].x, xx[b].y, xx[b].z, xx[b].w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                ax[2 * e] += bf16_to_f32(static_cast<uint16_t>(xw[e] & 0xffff));
+                ax[2 * e + 1] += bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
+              }
+            }
+        }
+      }
+      if (fin >= 0 && fin < a.MMB && g < ng) {
+        const float div = static_cast<float>(cnt) * static_cast<float>(bf);
+        const float inv = div > 0.0f ? 1.0f / div : 0.0f;
+        const int64_t hp = static_cast<int64_t>(h) * a.MMB + fin;
+        uint4 ox;
+        ox.x = pack_bf16x2(ax[0] * inv, ax[1] * inv);
+        ox.y = pack_bf16x2(ax[2] * inv, ax[3] * inv);
+        ox.z = pack_bf16x2(ax[4] * inv, ax[5] * inv);
+        ox.w = pack_bf16x2(ax[6] * inv, ax[7] * inv);
+        st16(merge_out + (hp * MTPA + g) * D + c, ox);
+        if (meta) {
+          int64_t *mp = ml.merge_pos + (hp * MTPA + g) * 3;
+          if (src_kind == kSrcGrid) {
+            mp[0] = sh.f_tpos[f];
+            mp[1] = (g / sh.grid_cols) * p;
+            mp[2] = (g % sh.grid_cols) * p;
+          } else {
+            const int64_t *ap = ml.accum_pos + (hs * MTPA + g) * 3;
+            const int64_t p0 = ap[0], p1 = ap[1], p2 = ap[2];
+            mp[0] = p0;
+            mp[1] = p1;
+            mp[2] = p2;
+          }
+        }
+      }
+    }
+    if (fin >= 0 && fin < a.MMB && mt == 0 && tid == 0) ml.merge_token_count[static_cast<int64_t>(h) * a.MMB + fin] = ng;
+  }
+  if (own && cur >= 0) store_acc(cur);
+}
+
+// Copy h's record into LDS (every thread; ends with a barrier)
+__device__ __forceinline__ void upd_stage(const UpdArgs &a, UpdShared &sh, int h) {
+  const uint32_t *gst = reinterpret_cast<const uint32_t *>(a.states + h);
+  if (threadIdx.x < kStateWords) reinterpret_cast<uint32_t *>(&sh.st)[threadIdx.x] = gst[threadIdx.x];
+  __syncthreads();
+}
+
+// Routing of head h from its committed counters, computed by every thread
+// from scalar reads (read before the head's last workgroup rewrites them)
+__device__ __forceinline__ Route upd_route(const UpdArgs &a, int h) {
+  const int64_t *cvc = a.committed_vc + h * 3;
+  return route_frames(ld_uniform(cvc), ld_uniform(cvc + 1), ld_uniform(cvc + 2), ld_uniform(a.sink_caps + h), a.F,
+                      a.max_sink, a.max_recent, a.shift_pending);
+}
+
+// Token tile `tile` of head h: thread = (token, 16-byte chunk), one item
+// per thread.  The routing needs only the committed counters, so the new
+// frames' chunks and the first recent slots the FIFO shift moves are loaded
+// at once; the record is staged and the state machine run only for heads
+// whose frames may go to middle slots (Wave, Anchor, lag).
+__device__ __forceinline__ void upd_token_tile(const UpdArgs &a, UpdShared &sh, int h, int tile) {
+  const int tid = threadIdx.x;
+  const int F = a.F, FSEQ = a.FSEQ, D = a.D;
+  const int cpt = D / 8, ttok = kUpdThreads / cpt;
+  const int tok = tile * ttok + tid / cpt, c = (tid % cpt) * 8;
+  const bool item = tid < ttok * cpt && tok < FSEQ;
+  const Route r = upd_route(a, h);
+  const int kind = ld_uniform(&a.states[h].kind);
+  const bool middle = a.pass_kind == 1 && (kind == SK_CYCLIC || kind == SK_STRIDE || kind == SK_LAG);
+  const int64_t lh = static_cast<int64_t>(a.layer) * a.H + h;
+  const int64_t slot_elems = static_cast<int64_t>(FSEQ) * D;
+  const uint32_t slot_b = static_cast<uint32_t>(slot_elems) * 2;
+  const PoolPtrs &pools = a.pools;
+  uint16_t *rec_k = pools.k[2] + lh * a.max_recent * slot_elems;
+  uint16_t *rec_v = pools.v[2] + lh * a.max_recent * slot_elems;
+  const uint32_t to = h * a.src_hb + tok * a.src_tb + c * 2;
+  const uint32_t e = (tok * D + c) * 2;
+  uint4 kk[kScatBatch], vv[kScatBatch], sk[kShiftBatch], sv[kShiftBatch];
+  if (item) {
+#pragma unroll
+    for (int f = 0; f < kScatBatch; ++f)
+      if (f < F) {
+        kk[f] = ld16o(a.src.k, to + f * a.src_fb);
+        vv[f] = ld16o(a.src.v, to + f * a.src_fb);
+      }
+#pragma unroll
+    for (int q = 0; q < kShiftBatch; ++q)
+      if (q < r.keep) {
+        sk[q] = ld16o(rec_k, (q + r.shift) * slot_b + e);
+        sv[q] = ld16o(rec_v, (q + r.shift) * slot_b + e);
+      }
+  }
+  if (middle) {  // uniform
+    upd_stage(a, sh, h);
+    if (tid == 0) upd_machine(a, sh);
+    __syncthreads();
+  }
+  if (tid == 0) {
+    sh.staged = middle;
+    sh.machine_done = middle;
+  }
+  uint16_t *sink_k = pools.k[0] + lh * a.max_sink * slot_elems;
+  uint16_t *sink_v = pools.v[0] + lh * a.max_sink * slot_elems;
+  uint16_t *mid_k = pools.k[1] + lh * a.max_middle * slot_elems;
+  uint16_t *mid_v = pools.v[1] + lh * a.max_middle * slot_elems;
+  const bool desc_ok = middle;
+  if (item) {
+    // recent FIFO shift: slot j <- slot j + shift for j < keep (all sources
+    // of a batch read before its stores; batches ascend, and a slot written
+    // by one batch is never a source of a later batch since sources are
+    // >= shift > destinations of earlier batches; the new frames are stored
+    // after every shift store)
+    for (int j0 = 0; j0 < r.keep; j0 += kShiftBatch) {
+      const int n = min(kShiftBatch, r.keep - j0);
+      if (j0 > 0) {
+#pragma unroll
+        for (int q = 0; q < kShiftBatch; ++q)
+          if (q < n) {
+            sk[q] = ld16o(rec_k, (j0 + q + r.shift) * slot_b + e);
+            sv[q] = ld16o(rec_v, (j0 + q + r.shift) * slot_b + e);
+          }
+      }
+#pragma unroll
+      for (int q = 0; q < kShiftBatch; ++q)
+        if (q < n) {
+          st16o(rec_k, (j0 + q) * slot_b + e, sk[q]);
+          st16o(rec_v, (j0 + q) * slot_b + e, sv[q]);
+        }
+    }
+    for (int f0 = 0; f0 < F; f0 += kScatBatch) {
+      const int n = min(kScatBatch, F - f0);
+      if (f0 > 0) {
+#pragma unroll
+        for (int q = 0; q < kScatBatch; ++q)
+          if (q < n) {
+            kk[q] = ld16o(a.src.k, to + (f0 + q) * a.src_fb);
+            vv[q] = ld16o(a.src.v, to + (f0 + q) * a.src_fb);
+          }
+      }
+#pragma unroll
+      for (int q = 0; q < kScatBatch; ++q) {
+        if (q >= n) continue;
+        const int f = f0 + q;
+        if (f < r.sink_writes) {
+          const uint32_t o = (r.sink_first + f) * slot_b + e;
+          st16o(sink_k, o, kk[q]);
+          st16o(sink_v, o, vv[q]);
+        } else {
+          const uint32_t o = (r.recent_first + (f - r.sink_writes)) * slot_b + e;
+          st16o(rec_k, o, kk[q]);
+          st16o(rec_v, o, vv[q]);
+        }
+        if (desc_ok && sh.desc[f].kind == PKV_DST_MIDDLE) {
+          const int s = sh.desc[f].slot;
+          if (s >= 0 && s < a.max_middle) {
+            st16o(mid_k, s * slot_b + e, kk[q]);
+            st16o(mid_v, s * slot_b + e, vv[q]);
+          }
+        }
+      }
+    }
+  }
+  // positions (t0 + f, tok / W, tok % W): one thread per token of the tile
+  const int pt = tile * ttok + tid;
+  if (tid < ttok && pt < FSEQ) {
+    const int64_t pe = static_cast<int64_t>(pt) * 3;
+    const int64_t pslot = static_cast<int64_t>(FSEQ) * 3;
+    int64_t *sink_p = pools.pos[0] + lh * a.max_sink * pslot;
+    int64_t *mid_p = pools.pos[1] + lh * a.max_middle * pslot;
+    int64_t *rec_p = pools.pos[2] + lh * a.max_recent * pslot;
+    for (int j = 0; j < r.keep; ++j) {
+      const int64_t *sp = rec_p + (j + r.shift) * pslot + pe;
+      const int64_t p0 = sp[0], p1 = sp[1], p2 = sp[2];
+      int64_t *dp = rec_p + j * pslot + pe;
+      dp[0] = p0;
+      dp[1] = p1;
+      dp[2] = p2;
+    }
+    const int64_t py = pt / a.width, px = pt % a.width;
+    for (int f = 0; f < F; ++f) {
+      const int64_t ptt = a.t0 + f;
+      int64_t *dp;
+      if (f < r.sink_writes)
+        dp = sink_p + (r.sink_first + f) * pslot + pe;
+      else
+        dp = rec_p + (r.recent_first + (f - r.sink_writes)) * pslot + pe;
+      dp[0] = ptt;
+      dp[1] = py;
+      dp[2] = px;
+      if (desc_ok && sh.desc[f].kind == PKV_DST_MIDDLE) {
+        const int64_t s = sh.desc[f].slot;
+        if (s >= 0 && s < a.max_middle) {
+          int64_t *mp = mid_p + s * pslot + pe;
+          mp[0] = ptt;
+          mp[1] = py;
+          mp[2] = px;
+        }
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
+  extern __shared__ int32_t dyn[];
+  __shared__ __attribute__((aligned(16))) UpdShared sh;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int F = a.F, FSEQ = a.FSEQ;
+  const bool merge_tile = b < a.H * a.n_merge;
+  const int h = merge_tile ? b / a.n_merge : (b - a.H * a.n_merge) / a.n_scat;
+  const int tile = merge_tile ? b % a.n_merge : (b - a.H * a.n_merge) % a.n_scat;
+  if (merge_tile) {
+    upd_stage(a, sh, h);
+    if (tid == 0) {
+      sh.staged = 1;
+      sh.machine_done = 0;
+      if (a.pass_kind == 1 && sh.st.kind == SK_MERGE) {
+        upd_machine(a, sh);
+        upd_merge_plan(a, h, sh);
+      }
+    }
+    __syncthreads();
+    if (sh.st.kind == SK_MERGE && a.pass_kind == 1) upd_merge_tile(a, h, tile, sh, dyn);
+  } else {
+    upd_token_tile(a, sh, h, tile);
+  }
+
+  // Arrival, after a barrier that follows every read of the head's shared
+  // data.  Tile i counts on sub-counter i % kArriveFan; the last arrival
+  // of each sub-counter counts on the head counter, and the last of those
+  // is the head's last workgroup.  Each counter sits on its own 128-byte
+  // line, so arrivals at one address stay few.
+  __syncthreads();
+  if (tid == 0) {
+    const int n_tiles = a.n_merge + a.n_scat;
+    const int idx = merge_tile ? tile : a.n_merge + tile;
+    const int sub = idx % kArriveFan;
+    const int sub_n = n_tiles / kArriveFan + (sub < n_tiles % kArriveFan ? 1 : 0);
+    const int n_sub = min(kArriveFan, n_tiles);
+    int32_t *ctr = a.arrive + static_cast<int64_t>(h) * (kArriveFan + 1) * kArriveStride;
+    int32_t *hc = ctr + kArriveFan * kArriveStride;
+    int last = 0;
+    if (atomicAdd(ctr + sub * kArriveStride, 1) == sub_n - 1) {
+      atomicExch(ctr + sub * kArriveStride, 0);
+      last = atomicAdd(hc, 1) == n_sub - 1;
+      if (last) atomicExch(hc, 0);
+    }
+    sh.last = last;
+  }
+  __syncthreads();
+  if (!sh.last) return;
+  if (!sh.staged) upd_stage(a, sh, h);  // uniform
+  const bool merge_head = a.n_merge > 0 && a.pass_kind == 1 && sh.st.kind == SK_MERGE;
+  if (tid == 0) {
+    if (!sh.machine_done) {
+      upd_machine(a, sh);
+      if (merge_head) upd_merge_plan(a, h, sh);
+    }
+    sh.r = upd_route(a, h);
+  }
+  __syncthreads();
+  if (a.pass_kind == 1 && tid < kStateWords)
+    reinterpret_cast<uint32_t *>(a.states + h)[tid] = reinterpret_cast<const uint32_t *>(&sh.st)[tid];
+  if (tid < 3) {
+    a.vc[h * 3 + tid] = sh.r.vc_post[tid];
+    if (a.pass_kind == 1) a.committed_vc[h * 3 + tid] = sh.r.vc_post[tid];
+  }
+  if (tid < F) store_desc(a.desc, h * F + tid, tid, h, sh.desc[tid]);
+  if (merge_head) {
+    const int p = sh.st.patch_size;
+    for (int s = 0; s < a.MMA; ++s) {
+      const int src = sh.s_src[s];
+      if (src == kSrcNone) continue;
+      const int64_t hs = static_cast<int64_t>(h) * a.MMA + s;
+      if (tid == 0) {
+        if (src == kSrcGrid) a.ml.accum_num_groups[hs] = sh.s_ng[s];
+        if (a.ml.accum_weight_sum) a.ml.accum_weight_sum[hs] = sh.s_wsum[s];
+      }
+      if (src == kSrcGrid)
+        for (int t = tid; t < FSEQ; t += blockDim.x)
+          a.ml.accum_group_ids[hs * FSEQ + t] = grid_gid(t, a.width, p, sh.grid_cols, sh.grid_ng);
+    }
+  }
+}
+
 // Scratch of pkv_merge_accum_static: the per-(head, frame) merge snapshots
 // (MergeWs) in a file-scope device array, for callers that cannot allocate.
 // Each device holds its own copy at its own address; host code never uses
@@ -1175,7 +1507,6 @@ int pkv_merge_accum(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, i
   ma.desc_new = desc_merge_is_new_block;
   ma.weights = frame_weights;
   ma.ml = *ml;
-  if (!frame_weights) ma.ml.accum_weight_sum = nullptr;
   ma.ws = carve_merge_ws(workspace, H, F, FSEQ, MTPA);
   ma.H = H; ma.F = F; ma.FSEQ = FSEQ; ma.D = D; ma.MMA = MMA; ma.MMB = MMB; ma.MTPA = MTPA;
   return launch_merge(ma, as_stream(stream));
@@ -1208,14 +1539,17 @@ int pkv_merge_accum_static(const uint8_t *states, int32_t H, int32_t F, int32_t 
                          frame_weights, ml, ws, stream);
 }
 
+// Workspace of pkv_cache_update: the 8 descriptor arrays ([H*F] int32 each,
+// 256-byte aligned) and the arrival counters (kArriveFan + 1 per head, one
+// 128-byte line each).
 static int64_t update_ws_bytes(int H, int F) {
-  return 8 * align_up(static_cast<int64_t>(H) * F * 4, 256) + align_up(static_cast<int64_t>(H) * sizeof(Route), 256);
+  return 8 * align_up(static_cast<int64_t>(H) * F * 4, 256) +
+         static_cast<int64_t>(H) * (kArriveFan + 1) * kArriveStride * 4;
 }
 
 int64_t pkv_cache_update_workspace_size(const pkv_geometry *geo, int32_t frames) {
   if (!geo || frames <= 0) return 0;
-  return update_ws_bytes(geo->num_heads, frames) +
-         merge_ws_bytes(geo->num_heads, frames, geo->frame_seqlen, geo->max_merge_tokens);
+  return update_ws_bytes(geo->num_heads, frames);
 }
 
 int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_update_args *a,
@@ -1225,60 +1559,76 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   if (!pools || !a || !a->new_k || !a->new_v || !a->states_layer || !a->sink_caps_layer ||
       !a->committed_vc_layer || !a->workspace)
     return fail(PKV_ERR_INVALID, "cache_update: NULL argument");
-  const int H = geo->num_heads, FSEQ = geo->frame_seqlen, D = geo->head_dim;
+  const int H = geo->num_heads, FSEQ = geo->frame_seqlen, D = geo->head_dim, F = a->frames;
   if (a->layer < 0 || a->layer >= geo->num_layers) return fail(PKV_ERR_INVALID, "cache_update: layer out of range");
-  if (a->frames <= 0 || a->frames > geo->max_recent)
-    return fail(PKV_ERR_UNSUPPORTED, "cache_update: frames per block (%d) must be in [1, max_recent=%d]",
-                a->frames, geo->max_recent);
+  if (F <= 0 || F > geo->max_recent)
+    return fail(PKV_ERR_UNSUPPORTED, "cache_update: frames per block (%d) must be in [1, max_recent=%d]", F,
+                geo->max_recent);
+  if (F > kUpdMaxFrames)
+    return fail(PKV_ERR_UNSUPPORTED, "cache_update: %d frames per block exceed %d", F, kUpdMaxFrames);
   if (a->spatial_width <= 0) return fail(PKV_ERR_INVALID, "cache_update: spatial_width must be > 0");
-  hipStream_t st = as_stream(stream);
-  Workspace ws = carve_workspace(a->workspace, H, a->frames);
-  int64_t *vc = pools->valid_count + static_cast<int64_t>(a->layer) * H * 3;
-  hipLaunchKernelGGL(route_kernel, dim3((H + kRouteHeads - 1) / kRouteHeads), dim3(kRouteThreads), 0, st,
-                     reinterpret_cast<HeadState *>(a->states_layer), H, a->frames, a->t0, a->pass_kind,
-                     a->shift_pending, geo->max_sink, geo->max_recent, a->sink_caps_layer,
-                     a->committed_vc_layer, vc, ws);
-  if ((rc = check_launch("route_kernel"))) return rc;
-  FrameSrc src{a->new_k, a->new_v, static_cast<int64_t>(FSEQ) * a->tok_stride, a->head_stride, a->tok_stride};
-  PosSrc pos{nullptr, a->t0, a->spatial_width, H, FSEQ};
-  ScatterArgs sa{src, pos, pool_ptrs(geo, pools), ws, a->layer, H, a->frames, FSEQ, D,
-                 geo->max_sink, geo->max_middle, geo->max_recent};
-  const int gx = (FSEQ + kScatTok - 1) / kScatTok;
-  if (!(a->pass_kind == 1 && a->has_merge_head)) {
-    hipLaunchKernelGGL(scatter_kernel, dim3(gx, H), dim3(256), 0, st, sa);
-    return check_launch("scatter_kernel");
-  }
+  if (D / 8 > kUpdThreads) return fail(PKV_ERR_UNSUPPORTED, "cache_update: head_dim %d exceeds %d", D, 8 * kUpdThreads);
   const int64_t l = a->layer;
   const int MMA = geo->max_merge_active, MMB = geo->max_merge_blocks, MTPA = geo->max_merge_tokens;
-  MergeArgs ma;
-  ma.states = reinterpret_cast<const HeadState *>(a->states_layer);
-  ma.src = src;
-  ma.pos = pos;
-  ma.desc_kind = ws.desc[0];
-  ma.desc_slot = ws.desc[4];
-  ma.desc_fin = ws.desc[6];
-  ma.desc_new = ws.desc[7];
-  ma.weights = nullptr;
-  ma.ml.accum_sum_k = pools->merge_accum_sum_k + l * H * MMA * MTPA * D;
-  ma.ml.accum_sum_v = pools->merge_accum_sum_v + l * H * MMA * MTPA * D;
-  ma.ml.accum_pos = pools->merge_accum_pos + l * H * MMA * MTPA * 3;
-  ma.ml.accum_group_ids = pools->merge_accum_group_ids + l * H * MMA * FSEQ;
-  ma.ml.accum_tokens_per_group = pools->merge_accum_tokens_per_group + l * H * MMA * MTPA;
-  ma.ml.accum_num_groups = pools->merge_accum_num_groups + l * H * MMA;
-  ma.ml.accum_weight_sum = nullptr;
-  ma.ml.merge_k = pools->merge_k + l * H * MMB * MTPA * D;
-  ma.ml.merge_v = pools->merge_v + l * H * MMB * MTPA * D;
-  ma.ml.merge_pos = pools->merge_pos + l * H * MMB * MTPA * 3;
-  ma.ml.merge_token_count = pools->merge_token_count + l * H * MMB;
-  ma.ws = carve_merge_ws(static_cast<char *>(a->workspace) + update_ws_bytes(H, a->frames), H, a->frames, FSEQ,
-                         MTPA);
-  ma.H = H; ma.F = a->frames; ma.FSEQ = FSEQ; ma.D = D; ma.MMA = MMA; ma.MMB = MMB; ma.MTPA = MTPA;
-  if ((rc = check_merge(ma))) return rc;
-  size_t smem;
-  if ((rc = merge_prep_smem(ma, reinterpret_cast<const void *>(scatter_merge_prep_kernel), smem))) return rc;
-  hipLaunchKernelGGL(scatter_merge_prep_kernel, dim3(gx * H + H), dim3(256), smem, st, sa, ma, gx, gx * H);
-  if ((rc = check_launch("scatter_merge_prep_kernel"))) return rc;
-  return launch_merge_accum(ma, st);
+  const bool merge = a->pass_kind == 1 && a->has_merge_head;
+  const int cpt = D / 8, per_tile = kUpdThreads / cpt;
+  UpdArgs u;
+  u.states = reinterpret_cast<HeadState *>(a->states_layer);
+  u.sink_caps = a->sink_caps_layer;
+  u.committed_vc = a->committed_vc_layer;
+  u.vc = pools->valid_count + l * H * 3;
+  u.src = FrameSrc{a->new_k, a->new_v, static_cast<int64_t>(FSEQ) * a->tok_stride, a->head_stride, a->tok_stride};
+  u.pools = pool_ptrs(geo, pools);
+  u.ml.accum_sum_k = pools->merge_accum_sum_k + l * H * MMA * MTPA * D;
+  u.ml.accum_sum_v = pools->merge_accum_sum_v + l * H * MMA * MTPA * D;
+  u.ml.accum_pos = pools->merge_accum_pos + l * H * MMA * MTPA * 3;
+  u.ml.accum_group_ids = pools->merge_accum_group_ids + l * H * MMA * FSEQ;
+  u.ml.accum_tokens_per_group = pools->merge_accum_tokens_per_group + l * H * MMA * MTPA;
+  u.ml.accum_num_groups = pools->merge_accum_num_groups + l * H * MMA;
+  u.ml.accum_weight_sum = pools->merge_accum_weight_sum ? pools->merge_accum_weight_sum + l * H * MMA : nullptr;
+  u.ml.merge_k = pools->merge_k + l * H * MMB * MTPA * D;
+  u.ml.merge_v = pools->merge_v + l * H * MMB * MTPA * D;
+  u.ml.merge_pos = pools->merge_pos + l * H * MMB * MTPA * 3;
+  u.ml.merge_token_count = pools->merge_token_count + l * H * MMB;
+  char *w = static_cast<char *>(a->workspace);
+  const int64_t dbytes = align_up(static_cast<int64_t>(H) * F * 4, 256);
+  int32_t *dw[8];
+  for (int i = 0; i < 8; ++i) dw[i] = reinterpret_cast<int32_t *>(w + i * dbytes);
+  u.desc = pkv_state_desc{dw[0], dw[1], dw[2], dw[3], dw[4], dw[5], dw[6], dw[7]};
+  u.arrive = reinterpret_cast<int32_t *>(w + 8 * dbytes);
+  const int64_t src_bytes = static_cast<int64_t>(F) * FSEQ * a->tok_stride * 2;
+  const int64_t max_slots = std::max(std::max(geo->max_sink, geo->max_middle), geo->max_recent);
+  if (src_bytes >= (int64_t{1} << 31) || max_slots * FSEQ * D * 2 >= (int64_t{1} << 31))
+    return fail(PKV_ERR_UNSUPPORTED, "cache_update: the new frames or one head's pool exceed 2 GiB");
+  u.src_fb = static_cast<uint32_t>(static_cast<int64_t>(FSEQ) * a->tok_stride * 2);
+  u.src_hb = static_cast<uint32_t>(a->head_stride * 2);
+  u.src_tb = static_cast<uint32_t>(a->tok_stride * 2);
+  u.t0 = a->t0;
+  u.layer = a->layer; u.H = H; u.F = F; u.FSEQ = FSEQ; u.D = D; u.width = a->spatial_width;
+  u.max_sink = geo->max_sink; u.max_middle = geo->max_middle; u.max_recent = geo->max_recent;
+  u.MMA = MMA; u.MMB = MMB; u.MTPA = MTPA;
+  u.pass_kind = a->pass_kind; u.shift_pending = a->shift_pending;
+  u.n_scat = (FSEQ + per_tile - 1) / per_tile;
+  u.n_merge = 0;
+  size_t smem = 0;
+  if (merge) {
+    if (FSEQ > kMaxMergeFseq)
+      return fail(PKV_ERR_UNSUPPORTED, "cache_update: frame_seqlen %d exceeds %d", FSEQ, kMaxMergeFseq);
+    if (MTPA > kMaxMergeGroups)
+      return fail(PKV_ERR_UNSUPPORTED, "cache_update: %d tokens per anchor exceed %d", MTPA, kMaxMergeGroups);
+    if (MMA > kMaxMergeSlots)
+      return fail(PKV_ERR_UNSUPPORTED, "cache_update: %d active merge blocks exceed %d", MMA, kMaxMergeSlots);
+    if (D / 8 > 64) return fail(PKV_ERR_UNSUPPORTED, "cache_update: merges need head_dim <= 512, got %d", D);
+    const int gpt = merge_tile_groups(D);
+    u.n_merge = (MTPA + gpt - 1) / gpt;
+    smem = static_cast<size_t>(tile_list_words(FSEQ, gpt)) * sizeof(int32_t);
+    if (smem > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(update_kernel),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(smem)) != hipSuccess)
+      return fail(PKV_ERR_HIP, "cache_update: cannot reserve %zu bytes of LDS", smem);
+  }
+  hipLaunchKernelGGL(update_kernel, dim3(H * (u.n_merge + u.n_scat)), dim3(kUpdThreads), smem, as_stream(stream), u);
+  return check_launch("update_kernel");
 }
 
 }  // extern "C"

@@ -56,6 +56,19 @@ def _compare_pools(caches, ref: O.MegaCacheRef, where: str):
             raise AssertionError(f"{where}: {name} differs at {len(bad)} places, first {bad[:4].tolist()}")
     got_states = to_np(caches[0].ctx.states_bytes).reshape(ref.states.shape)
     assert np.array_equal(got_states, ref.states), f"{where}: state records differ"
+    # Veil accumulators: fp32 group sums, group ids / counts / positions, weight sums
+    accs = [("sum_k", mgr.merge_accum_sum_k()), ("sum_v", mgr.merge_accum_sum_v()), ("pos", mgr.merge_accum_pos()),
+            ("gid", mgr.merge_accum_group_ids()), ("tpg", mgr.merge_accum_tokens_per_group()),
+            ("ng", mgr.merge_accum_num_groups()), ("wsum", mgr.merge_accum_weight_sum())]
+    for name, t in accs:
+        got = to_np(t)
+        for layer, acc in enumerate(ref.acc):
+            want = acc[name]
+            g = got[layer].reshape(want.shape)
+            if not np.array_equal(g, want):
+                bad = np.argwhere(g != want)
+                raise AssertionError(f"{where}: merge accumulator {name} of layer {layer} differs at {len(bad)} "
+                                     f"places, first {bad[:4].tolist()}")
 
 
 def _compare_attend(cache, ref: O.MegaCacheRef, layer, start, chunks, q_u16, where):
@@ -99,16 +112,20 @@ def _rand_bf16(rng, *shape):
     return O.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))
 
 
-@pytest.mark.parametrize("seed,block_sizes,noisy_passes", [
-    (0, [3] * 9, 2),
-    (1, [1] + [3] * 8, 1),
-    (2, [2, 2, 3, 1, 3, 3, 2, 3, 4], 3),
+# (FS, W): 64 / 8 tiles into the Veil heads' 2 x 2 patches (member lists in
+# closed form); 63 / 9 does not (odd width: lists built from the group ids)
+@pytest.mark.parametrize("seed,block_sizes,noisy_passes,FS,W", [
+    (0, [3] * 9, 2, 64, 8),
+    (1, [1] + [3] * 8, 1, 64, 8),
+    (2, [2, 2, 3, 1, 3, 3, 2, 3, 4], 3, 64, 8),
+    (3, [3] * 6, 1, 63, 9),
+    (4, [2, 3, 1, 4, 3, 2], 2, 63, 9),
 ])
-def test_megacache_rollout_bit_exact(seed, block_sizes, noisy_passes):
+def test_megacache_rollout_bit_exact(seed, block_sizes, noisy_passes, FS, W):
     rng = np.random.default_rng(seed)
-    L, H, D, FS, W = 2, 6, 128, 64, 8
+    L, H, D = 2, 6, 128
     labels = [[-1, 1, 2, -1, 1, 2], [2, -1, 1, 1, 2, -1]]
-    print(f"megacache rollout seed={seed} blocks={block_sizes} noisy={noisy_passes}", flush=True)
+    print(f"megacache rollout seed={seed} blocks={block_sizes} noisy={noisy_passes} FS={FS} W={W}", flush=True)
     caches, ref, g = _build(L, H, D, FS, W, labels, chunks=4)
     t0 = 0
     for bi, F in enumerate(block_sizes):
@@ -129,6 +146,45 @@ def test_megacache_rollout_bit_exact(seed, block_sizes, noisy_passes):
             torch.cuda.synchronize()
             _compare_pools(caches, ref, f"block {bi} pass {p} {mode}")
         t0 += F
+
+
+@pytest.mark.parametrize("how", ["permuted", "other_width"])
+def test_megacache_continues_block_by_its_stored_group_ids(how):
+    """A Veil block whose stored group ids are not the ids of the update's
+    grid -- as when the block began through mega_merge_accum with explicit
+    positions -- continues through MegaCache.update by the stored ids, as
+    the reference's accumulate does (mega_merge_accum.cu:193-209).  The ids
+    are replaced in the device pools and in the oracle alike between two
+    updates: a token permutation of the grid ids, or the ids of a grid of
+    another width with the same group count."""
+    rng = np.random.default_rng(11)
+    L, H, D, FS, W, F = 1, 2, 128, 64, 8, 3
+    print(f"stored group ids ({how})", flush=True)
+    caches, ref, g = _build(L, H, D, FS, W, [[2, 2]], chunks=F)
+    mgr = caches[0].ctx.mgr
+
+    def step(t0):
+        k, v = _rand_bf16(rng, F * FS, H, D), _rand_bf16(rng, F * FS, H, D)
+        caches[0].update(to_dev(k).view(torch.bfloat16).view(1, F * FS, H, D),
+                         to_dev(v).view(torch.bfloat16).view(1, F * FS, H, D), t0 * FS, cache_update_mode="clean")
+        ref.update(0, k, v, t0 * FS, "clean")
+
+    step(0)  # frames 0-2 begin block 0 (4 frames) of every head
+    torch.cuda.synchronize()
+    slot = int(to_np(caches[0].last_update_descriptors(F)[4])[0])
+    gid = ref.acc[0]["gid"]
+    if how == "permuted":
+        new_ids = gid[:, slot, ::-1].copy()
+    else:  # the 2 x 2 patches of a 16-wide grid: 2 x 8 groups, as many as 4 x 4
+        t = np.arange(FS)
+        new_ids = np.broadcast_to(((t // 16) // 2) * 8 + (t % 16) // 2, (H, FS)).astype(np.int32).copy()
+    assert not np.array_equal(new_ids, gid[:, slot])
+    gid[:, slot] = new_ids
+    mgr.merge_accum_group_ids()[0, :, slot].copy_(to_dev(new_ids))
+    step(3)  # frame 3 completes block 0 through the stored ids; frames 4-5 begin block 1
+    torch.cuda.synchronize()
+    _compare_pools(caches, ref, f"after the continued block ({how})")
+    assert int(to_np(mgr.merge_token_count())[0, 0].max()) > 0, "block 0 was finalized"
 
 
 def test_megacache_rejects_update_of_new_block_while_noisy_pending():
