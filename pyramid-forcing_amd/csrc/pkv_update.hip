@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "pkv_common.h"
 #include "pkv_state_machine.h"
@@ -811,6 +812,11 @@ constexpr int kScatBatch = 4;   // new frames loaded per batch
 constexpr int kShiftBatch = 2;  // shifted recent slots loaded per batch
 constexpr int kUpdAccBatch = 4; // member tokens loaded per batch by a merge tile
 constexpr int kStateWords = static_cast<int>(sizeof(HeadState) / 4);
+
+// A value every lane holds alike (read from LDS after a barrier), made
+// visibly uniform so that branches on it stay scalar branches and the code
+// on either side shares registers
+__device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 constexpr int kArriveFan = 8;      // arrival sub-counters per head
 constexpr int kArriveStride = 32;  // int32 words between counters (128 bytes)
 
@@ -901,6 +907,8 @@ struct UpdShared {
   FrameDesc desc[kUpdMaxFrames];
   Route r;
   int32_t staged, machine_done, last;
+  int32_t g_ng[kMaxMergeSlots];  // stored group counts and weight sums of the slots
+  float g_wsum[kMaxMergeSlots];
   // merge bookkeeping: per frame, the list source and group count of its
   // block; per slot, the source, group count and weight sum after the call
   // and the stored-id check (-1 not done, 0 not the regular grid, else its
@@ -952,7 +960,6 @@ __device__ void upd_merge_plan(const UpdArgs &a, int h, UpdShared &sh) {
     sh.f_src[f] = kSrcNone;
     if (d.kind != PKV_DST_MERGE_ACCUM || d.accum_slot < 0 || d.accum_slot >= a.MMA) continue;
     const int s = d.accum_slot;
-    const int64_t hs = static_cast<int64_t>(h) * a.MMA + s;
     if (d.is_new_block) {
       sh.s_src[s] = kSrcGrid;
       sh.s_ng[s] = sh.grid_ng;
@@ -960,9 +967,9 @@ __device__ void upd_merge_plan(const UpdArgs &a, int h, UpdShared &sh) {
       sh.s_wsum[s] = 0.0f;
     } else if (sh.s_src[s] == kSrcNone) {
       sh.s_src[s] = s;
-      sh.s_ng[s] = min(a.ml.accum_num_groups[hs], MTPA);
+      sh.s_ng[s] = min(sh.g_ng[s], MTPA);
       sh.s_tpos[s] = 0;
-      sh.s_wsum[s] = a.ml.accum_weight_sum ? a.ml.accum_weight_sum[hs] : 0.0f;
+      sh.s_wsum[s] = sh.g_wsum[s];
     }
     sh.s_wsum[s] += 1.0f;
     sh.f_src[f] = sh.s_src[s];
@@ -985,32 +992,6 @@ __device__ int stored_grid_width(const int32_t *gids, int FSEQ, int W, int p, in
   return ok && !any_bad ? W : 0;
 }
 
-// LDS words of a merge tile's lists: local ids and members [FSEQ] each,
-// starts [gpt + 2], per-wave counts [kMergeWaves * (gpt + 1)], scan partials
-__host__ __device__ inline int64_t tile_list_words(int FSEQ, int gpt) {
-  return 2 * static_cast<int64_t>(FSEQ) + (gpt + 2) + kMergeWaves * static_cast<int64_t>(gpt + 1) + kUpdThreads;
-}
-
-// Member lists of groups [g0, g0 + gpt) in ascending token order (the
-// reference's accumulation order) from the call's grid ids (src ==
-// kSrcGrid) or the ids stored for slot src: a stable CSR over gpt + 1 local
-// groups, the last one collecting every other token.
-__device__ void tile_lists(const UpdArgs &a, const UpdShared &sh, int src, int h, int g0, int gpt, int32_t *dyn) {
-  int32_t *lid = dyn, *members = lid + a.FSEQ, *gstart = members + a.FSEQ;
-  int32_t *cntw = gstart + gpt + 2, *part = cntw + kMergeWaves * (gpt + 1);
-  const int p = sh.st.patch_size;
-  const int32_t *stored =
-      src >= 0 ? a.ml.accum_group_ids + (static_cast<int64_t>(h) * a.MMA + src) * a.FSEQ : nullptr;
-  __syncthreads();  // readers of the previous lists are done
-  for (int t = threadIdx.x; t < a.FSEQ; t += blockDim.x) {
-    const int g = stored ? stored[t] : grid_gid(t, a.width, p, sh.grid_cols, sh.grid_ng);
-    const int l = g - g0;
-    lid[t] = (l >= 0 && l < gpt) ? l : gpt;
-  }
-  __syncthreads();
-  build_csr(lid, a.FSEQ, gpt + 1, cntw, gstart, members, part);
-}
-
 // Merge tile mt of head h: groups [mt * gpt, (mt + 1) * gpt), thread =
 // (group, 8-wide dim chunk), every accumulator element owned by one thread
 // for all frames (mega_merge_accum.cu:52-252).  Per frame in order: a slot
@@ -1022,51 +1003,223 @@ __device__ void tile_lists(const UpdArgs &a, const UpdShared &sh, int src, int h
 // waves) or V (odd waves), the wave pairs side by side
 __host__ __device__ inline int merge_tile_groups(int D) { return (kUpdThreads / 128) * (64 / (D / 8)); }
 
-__device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, int32_t *dyn) {
+// Dynamic LDS of a merge tile (int32 words): the group ids its scan reads
+// [FSEQ], the stored group ids of every accumulator slot [MMA][FSEQ] and,
+// with at most kStagedSlots slots, the accumulators this tile's threads own
+// [MMA][kUpdThreads][8] (fp32); each region starts on a 16-byte boundary.
+constexpr int kStagedSlots = 2;
+constexpr bool kStageAccumulators = false;
+__host__ __device__ inline int merge_fseq_words(int FSEQ) { return (FSEQ + 3) & ~3; }
+__host__ __device__ inline int64_t merge_lds_words(int FSEQ, int MMA) {
+  const int64_t fw = merge_fseq_words(FSEQ);
+  return fw * (1 + MMA) + (MMA <= kStagedSlots ? static_cast<int64_t>(MMA) * kUpdThreads * 8 : 0);
+}
+
+// Patch chunks of a merge tile's groups in every frame of a call, loaded
+// before the record is staged and the state machine run: the members of a
+// group on the regular grid of width W = min(spatial width, FSEQ) depend on
+// nothing else.  merge_prefetch returns W, or 0 when the call does not
+// qualify (then nothing is loaded); frames whose lists turn out otherwise
+// load their members themselves.
+constexpr int kPreFrames = 3;
+constexpr int kPreTok = 4;
+struct MergePre {
+  uint4 x[kPreFrames][kPreTok];
+};
+
+// thread -> (group, K or V, 8-wide chunk) of merge tile mt, shared by the
+// prefetch and the tile
+struct MergeLane {
+  int g, c, is_v, own;
+  __device__ MergeLane(const UpdArgs &a, int mt) {
+    const int cpt = a.D / 8, gpw = 64 / cpt;
+    const int wave = static_cast<int>(threadIdx.x) >> 6, lane = static_cast<int>(threadIdx.x) & 63;
+    is_v = wave & 1;  // wave-uniform: K or V
+    g = mt * merge_tile_groups(a.D) + (wave >> 1) * gpw + lane / cpt;
+    c = (lane % cpt) * 8;
+    own = lane / cpt < gpw && g < a.MTPA;
+  }
+};
+
+__device__ __forceinline__ int merge_prefetch(const UpdArgs &a, int h, int mt, MergePre &pre) {
+  const int p = ld_uniform(&a.states[h].patch_size);
+  const int kind = ld_uniform(&a.states[h].kind);
+  const int FSEQ = a.FSEQ, W = min(a.width, FSEQ);
+  if (kind != SK_MERGE || a.F > kPreFrames || p <= 0 || p * p > kPreTok || FSEQ % W != 0 || W % p != 0 ||
+      (FSEQ / W) % p != 0)
+    return 0;
+  const MergeLane ln(a, mt);
+  if (ln.own && ln.g < FSEQ / (p * p)) {
+    const uint16_t *src = ln.is_v ? a.src.v : a.src.k;
+    const int gcols = W / p;
+    const int gbase = (ln.g / gcols) * p * W + (ln.g % gcols) * p;
+#pragma unroll
+    for (int f = 0; f < kPreFrames; ++f)
+#pragma unroll
+      for (int m = 0; m < kPreTok; ++m)
+        if (f < a.F && m < p * p)
+          pre.x[f][m] = ld16o(src, f * a.src_fb + h * a.src_hb + ln.c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb);
+  }
+  return W;
+}
+
+// Merge tiles stage the stored group ids of every slot and, with at most
+// kStagedSlots slots, their threads' accumulators into LDS with the record
+// (one round trip for everything a tile reads; upd_stage's barrier orders
+// the LDS writes)
+__device__ __forceinline__ void merge_stage(const UpdArgs &a, int h, const MergeLane &ln, int32_t *dyn) {
+  const int tid = threadIdx.x, FSEQ = a.FSEQ, fw = merge_fseq_words(FSEQ);
+  const int n = a.MMA * FSEQ;
+  const int32_t *gids = a.ml.accum_group_ids + static_cast<int64_t>(h) * a.MMA * FSEQ;
+  constexpr int kB = 8;
+  for (int i0 = 0; i0 < n; i0 += kB * kUpdThreads) {
+    int32_t v[kB];
+#pragma unroll
+    for (int k = 0; k < kB; ++k) v[k] = gids[min(i0 + tid + k * kUpdThreads, n - 1)];
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = i0 + tid + k * kUpdThreads;
+      if (i < n) dyn[fw + (i / FSEQ) * fw + i % FSEQ] = v[k];
+    }
+  }
+  if (kStageAccumulators && a.MMA <= kStagedSlots && ln.own) {
+    const float *acc_sum = ln.is_v ? a.ml.accum_sum_v : a.ml.accum_sum_k;
+    float4 *accl = reinterpret_cast<float4 *>(dyn + fw * (1 + a.MMA));
+    float4 x[kStagedSlots][2];
+#pragma unroll
+    for (int s = 0; s < kStagedSlots; ++s)
+      if (s < a.MMA) {
+        const float4 *src = reinterpret_cast<const float4 *>(
+            acc_sum + ((static_cast<int64_t>(h) * a.MMA + s) * a.MTPA + ln.g) * a.D + ln.c);
+        x[s][0] = src[0];
+        x[s][1] = src[1];
+      }
+#pragma unroll
+    for (int s = 0; s < kStagedSlots; ++s)
+      if (s < a.MMA) {
+        accl[(s * kUpdThreads + tid) * 2] = x[s][0];
+        accl[(s * kUpdThreads + tid) * 2 + 1] = x[s][1];
+      }
+  }
+}
+
+__device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, int32_t *dyn, const MergePre &pre,
+                               int spec) {
   const int tid = threadIdx.x, D = a.D, MTPA = a.MTPA, FSEQ = a.FSEQ;
-  const int cpt = D / 8, gpw = 64 / cpt, gpt = merge_tile_groups(D);
-  const int wave = tid >> 6, lane = tid & 63;
-  const int is_v = wave & 1;  // wave-uniform: K or V
-  const int gl = (wave >> 1) * gpw + lane / cpt, c = (lane % cpt) * 8;
-  const int g = mt * gpt + gl;
-  const bool own = lane / cpt < gpw && g < MTPA;
-  const bool meta = own && !is_v && c == 0;  // writes the group's count and positions
+  const MergeLane ln(a, mt);
+  const int g = ln.g, c = ln.c;
+  const bool own = ln.own;
+  const bool meta = own && !ln.is_v && c == 0;  // writes the group's count and positions
   const int32_t p = sh.st.patch_size, bf = sh.st.block_frames;
   const pkv_merge_layer &ml = a.ml;
-  const uint16_t *src = is_v ? a.src.v : a.src.k;
-  float *acc_sum = is_v ? ml.accum_sum_v : ml.accum_sum_k;
-  uint16_t *merge_out = is_v ? ml.merge_v : ml.merge_k;
-  const int32_t *members = dyn + FSEQ, *gstart = members + FSEQ;
+  const uint16_t *src = ln.is_v ? a.src.v : a.src.k;
+  float *acc_sum = ln.is_v ? ml.accum_sum_v : ml.accum_sum_k;
+  uint16_t *merge_out = ln.is_v ? ml.merge_v : ml.merge_k;
   float ax[8];
   int cur = -1;
-  int list_src = kSrcNone;  // source of the CSR lists in LDS
+  uint32_t touched = 0;    // slots whose accumulators this call has moved
+  int ids_src = kSrcNone;  // source of the group ids the scan reads
   auto store_acc = [&](int slot) {
     const int64_t o = ((static_cast<int64_t>(h) * a.MMA + slot) * MTPA + g) * D + c;
     for (int e = 0; e < 8; ++e) acc_sum[o + e] = ax[e];
   };
-  for (int f = 0; f < a.F; ++f) {
+  // one member chunk added to the accumulators (one fp32 add per element)
+  auto add16 = [&](const uint4 &x) {
+    const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ax[2 * e] += bf16_to_f32(static_cast<uint16_t>(xw[e] & 0xffff));
+      ax[2 * e + 1] += bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
+    }
+  };
+  // Width of the regular grid whose closed-form lists frame f's block
+  // uses, or 0 (all threads: the first use of a stored slot votes on its ids)
+  auto frame_width = [&](int f) {
     const int src_kind = sh.f_src[f];
-    if (src_kind == kSrcNone) continue;
-    const uint32_t fo = f * a.src_fb + h * a.src_hb + c * 2;
+    if (src_kind == kSrcGrid) return sh.grid_w;
+    if (sh.s_grid[src_kind] < 0) {
+      const int64_t hs = static_cast<int64_t>(h) * a.MMA + src_kind;
+      sh.s_grid[src_kind] =
+          stored_grid_width(dyn + merge_fseq_words(FSEQ) * (1 + src_kind), FSEQ, min(a.width, FSEQ), p, sh.f_ng[f]);
+    }
+    return sh.s_grid[src_kind];
+  };
+  // Merge frame f.  kClosed: the lists are the closed form of width spec
+  // and pf holds the patch's chunks, loaded up front.  Otherwise, on a
+  // regular grid of width W the members are loaded here, and without one
+  // each thread scans the block's group ids (staged in LDS) for its group's
+  // tokens in ascending order -- the path of grids that do not tile into
+  // patches and of blocks begun with other positions.
+  auto frame = [&](int f, const uint4 *pf, auto closed_tag) {
+    constexpr bool kClosed = decltype(closed_tag)::value;
+    const int src_kind = sh.f_src[f];
+    if (src_kind == kSrcNone) return;
     const FrameDesc d = sh.desc[f];
     const int slot = d.accum_slot, is_new = d.is_new_block, fin = d.finalize_idx;
     const int ng = sh.f_ng[f];
     const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
-    // the block's lists: closed form on a regular grid of width W, else CSR
-    int W;
-    if (src_kind == kSrcGrid) {
-      W = sh.grid_w;
-    } else {
-      if (sh.s_grid[src_kind] < 0)
-        sh.s_grid[src_kind] = stored_grid_width(ml.accum_group_ids + hs * FSEQ, FSEQ, min(a.width, FSEQ), p, ng);
-      W = sh.s_grid[src_kind];
-    }
-    if (W == 0 && list_src != src_kind) {
-      tile_lists(a, sh, src_kind, h, mt * gpt, gpt, dyn);
-      list_src = src_kind;
+    int W = spec;
+    if constexpr (!kClosed) {
+      W = frame_width(f);
+      if (uni(W == 0 && ids_src != src_kind)) {
+        if (src_kind == kSrcGrid) {  // stored ids are staged already
+          __syncthreads();  // readers of the previous ids are done
+          for (int t = tid; t < FSEQ; t += blockDim.x) dyn[t] = grid_gid(t, a.width, p, sh.grid_cols, sh.grid_ng);
+          __syncthreads();
+        }
+        ids_src = src_kind;
+      }
     }
     if (own) {
-      const int cnt = W ? p * p : gstart[gl + 1] - gstart[gl];
+      if (slot != cur) {
+        if (cur >= 0) store_acc(cur);
+        cur = slot;
+        if (!is_new) {
+          if (kStageAccumulators && a.MMA <= kStagedSlots && !((touched >> slot) & 1)) {  // as staged
+            const float *accl = reinterpret_cast<const float *>(dyn + merge_fseq_words(FSEQ) * (1 + a.MMA)) +
+                                (slot * kUpdThreads + tid) * 8;
+            for (int e = 0; e < 8; ++e) ax[e] = accl[e];
+          } else {
+            const int64_t o = (hs * MTPA + g) * D + c;
+            for (int e = 0; e < 8; ++e) ax[e] = acc_sum[o + e];
+          }
+        }
+        touched |= 1u << slot;
+      }
+      if (is_new)
+        for (int e = 0; e < 8; ++e) ax[e] = 0.0f;
+      int cnt = p * p;  // members of group g
+      if (g < ng) {
+        if constexpr (kClosed) {
+#pragma unroll
+          for (int m = 0; m < kPreTok; ++m)
+            if (m < p * p) add16(pf[m]);
+        } else {
+          const uint32_t fo = f * a.src_fb + h * a.src_hb + c * 2;
+          if (W) {
+            const int gcols = W / p;
+            const int gbase = (g / gcols) * p * W + (g % gcols) * p;
+            for (int mb = 0; mb < p * p; mb += kUpdAccBatch) {
+              const int n = min(kUpdAccBatch, p * p - mb);
+              uint4 xx[kUpdAccBatch];
+#pragma unroll
+              for (int b = 0; b < kUpdAccBatch; ++b)
+                if (b < n) xx[b] = ld16o(src, fo + (gbase + ((mb + b) / p) * W + (mb + b) % p) * a.src_tb);
+#pragma unroll
+              for (int b = 0; b < kUpdAccBatch; ++b)
+                if (b < n) add16(xx[b]);
+            }
+          } else {
+            const int32_t *ids = src_kind == kSrcGrid ? dyn : dyn + merge_fseq_words(FSEQ) * (1 + src_kind);
+            cnt = 0;
+            for (int t = 0; t < FSEQ; ++t)
+              if (ids[t] == g) {
+                add16(ld16o(src, fo + t * a.src_tb));
+                ++cnt;
+              }
+          }
+        }
+      }
       if (is_new && meta) {
         ml.accum_tokens_per_group[hs * MTPA + g] = g < ng ? static_cast<float>(cnt) * static_cast<float>(bf) : 0.0f;
         if (g < ng) {
@@ -1074,42 +1227,6 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
           ap[0] = sh.f_tpos[f];
           ap[1] = (g / sh.grid_cols) * p;
           ap[2] = (g % sh.grid_cols) * p;
-        }
-      }
-      if (slot != cur) {
-        if (cur >= 0) store_acc(cur);
-        cur = slot;
-        if (!is_new) {
-          const int64_t o = (hs * MTPA + g) * D + c;
-          for (int e = 0; e < 8; ++e) ax[e] = acc_sum[o + e];
-        }
-      }
-      if (is_new)
-        for (int e = 0; e < 8; ++e) ax[e] = 0.0f;
-      if (g < ng) {
-        const int gcols = W ? W / p : 1;
-        const int gbase = W ? (g / gcols) * p * W + (g % gcols) * p : 0;
-        const int m0 = W ? 0 : gstart[gl], m1 = W ? p * p : gstart[gl + 1];
-        for (int mb = m0; mb < m1; mb += kUpdAccBatch) {
-          const int n = min(kUpdAccBatch, m1 - mb);
-          uint4 xx[kUpdAccBatch];
-#pragma unroll
-          for (int b = 0; b < kUpdAccBatch; ++b)
-            if (b < n) {
-              const int m = mb + b;
-              const int tok = W ? gbase + (m / p) * W + m % p : members[m];
-              xx[b] = ld16o(src, fo + tok * a.src_tb);
-            }
-#pragma unroll
-          for (int b = 0; b < kUpdAccBatch; ++b)
-            if (b < n) {
-              const uint32_t xw[4] = {xx[b].x, xx[b].y, xx[b].z, xx[b].w};
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                ax[2 * e] += bf16_to_f32(static_cast<uint16_t>(xw[e] & 0xffff));
-                ax[2 * e + 1] += bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
-              }
-            }
         }
       }
       if (fin >= 0 && fin < a.MMB && g < ng) {
@@ -1139,14 +1256,63 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
       }
     }
     if (fin >= 0 && fin < a.MMB && mt == 0 && tid == 0) ml.merge_token_count[static_cast<int64_t>(h) * a.MMB + fin] = ng;
+  };
+  // the prefetched chunks serve when every merge frame's lists are the
+  // closed form of width spec (uniform)
+  bool closed = spec != 0;
+  for (int f = 0; f < a.F && closed; ++f)
+    if (sh.f_src[f] != kSrcNone) closed = frame_width(f) == spec;
+  if (uni(closed)) {
+#pragma unroll
+    for (int f = 0; f < kPreFrames; ++f)
+      if (f < a.F) frame(f, pre.x[f], std::true_type{});
+  } else {
+    for (int f = 0; f < a.F; ++f) frame(f, nullptr, std::false_type{});
   }
   if (own && cur >= 0) store_acc(cur);
 }
 
+// Arrival of tile idx of head h, in two levels: tile idx counts on
+// sub-counter idx % kArriveFan, the last arrival of each sub-counter counts
+// on the head counter, and the last of those is the head's last workgroup.
+// Each counter sits on its own 128-byte line, so arrivals at one address
+// stay few.  arrive_take (thread 0) returns the sub-counter's previous
+// value; arrive_last resolves it, resetting every counter it completes.
+__device__ inline int32_t *arrive_counters(const UpdArgs &a, int h) {
+  return a.arrive + static_cast<int64_t>(h) * (kArriveFan + 1) * kArriveStride;
+}
+
+__device__ inline int arrive_take(const UpdArgs &a, int h, int idx) {
+  return atomicAdd(arrive_counters(a, h) + (idx % kArriveFan) * kArriveStride, 1);
+}
+
+__device__ inline int arrive_last(const UpdArgs &a, int h, int idx, int ticket) {
+  const int n_tiles = a.n_merge + a.n_scat;
+  const int sub = idx % kArriveFan;
+  const int sub_n = n_tiles / kArriveFan + (sub < n_tiles % kArriveFan ? 1 : 0);
+  if (ticket != sub_n - 1) return 0;
+  int32_t *ctr = arrive_counters(a, h);
+  atomicExch(ctr + sub * kArriveStride, 0);
+  int32_t *hc = ctr + kArriveFan * kArriveStride;
+  const int last = atomicAdd(hc, 1) == min(kArriveFan, n_tiles) - 1;
+  if (last) atomicExch(hc, 0);
+  return last;
+}
+
 // Copy h's record into LDS (every thread; ends with a barrier)
 __device__ __forceinline__ void upd_stage(const UpdArgs &a, UpdShared &sh, int h) {
-  const uint32_t *gst = reinterpret_cast<const uint32_t *>(a.states + h);
-  if (threadIdx.x < kStateWords) reinterpret_cast<uint32_t *>(&sh.st)[threadIdx.x] = gst[threadIdx.x];
+  // with the record, on a clean pass of a layer with merges, the stored
+  // group counts and weight sums of h's accumulator slots: one round trip
+  const int tid = threadIdx.x;
+  const int64_t hs0 = static_cast<int64_t>(h) * a.MMA;
+  if (tid < kStateWords) {
+    reinterpret_cast<uint32_t *>(&sh.st)[tid] = reinterpret_cast<const uint32_t *>(a.states + h)[tid];
+  } else if (a.n_merge > 0 && tid < kStateWords + a.MMA) {
+    sh.g_ng[tid - kStateWords] = a.ml.accum_num_groups[hs0 + tid - kStateWords];
+  } else if (a.n_merge > 0 && tid < kStateWords + 2 * a.MMA) {
+    const int s = tid - kStateWords - a.MMA;
+    sh.g_wsum[s] = a.ml.accum_weight_sum ? a.ml.accum_weight_sum[hs0 + s] : 0.0f;
+  }
   __syncthreads();
 }
 
@@ -1163,7 +1329,7 @@ __device__ __forceinline__ Route upd_route(const UpdArgs &a, int h) {
 // frames' chunks and the first recent slots the FIFO shift moves are loaded
 // at once; the record is staged and the state machine run only for heads
 // whose frames may go to middle slots (Wave, Anchor, lag).
-__device__ __forceinline__ void upd_token_tile(const UpdArgs &a, UpdShared &sh, int h, int tile) {
+__device__ __forceinline__ void upd_token_tile(const UpdArgs &a, UpdShared &sh, int h, int tile, int &ticket) {
   const int tid = threadIdx.x;
   const int F = a.F, FSEQ = a.FSEQ, D = a.D;
   const int cpt = D / 8, ttok = kUpdThreads / cpt;
@@ -1203,7 +1369,13 @@ __device__ __forceinline__ void upd_token_tile(const UpdArgs &a, UpdShared &sh, 
   if (tid == 0) {
     sh.staged = middle;
     sh.machine_done = middle;
+    sh.r = r;
   }
+  // every read of the head's shared data (its record and committed
+  // counters) is done: arrive now, so that the head's write-back overlaps
+  // the stores below
+  __syncthreads();
+  if (tid == 0) ticket = arrive_take(a, h, a.n_merge + tile);
   uint16_t *sink_k = pools.k[0] + lh * a.max_sink * slot_elems;
   uint16_t *sink_v = pools.v[0] + lh * a.max_sink * slot_elems;
   uint16_t *mid_k = pools.k[1] + lh * a.max_middle * slot_elems;
@@ -1314,56 +1486,42 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
   const bool merge_tile = b < a.H * a.n_merge;
   const int h = merge_tile ? b / a.n_merge : (b - a.H * a.n_merge) / a.n_scat;
   const int tile = merge_tile ? b % a.n_merge : (b - a.H * a.n_merge) % a.n_scat;
+  int ticket = 0;  // thread 0: the arrival sub-counter's previous value
   if (merge_tile) {
+    const Route r = upd_route(a, h);
+    MergePre pre;
+    const int spec = a.pass_kind == 1 ? merge_prefetch(a, h, tile, pre) : 0;
+    merge_stage(a, h, MergeLane(a, tile), dyn);
     upd_stage(a, sh, h);
     if (tid == 0) {
       sh.staged = 1;
       sh.machine_done = 0;
+      sh.r = r;
       if (a.pass_kind == 1 && sh.st.kind == SK_MERGE) {
         upd_machine(a, sh);
         upd_merge_plan(a, h, sh);
       }
     }
     __syncthreads();
-    if (sh.st.kind == SK_MERGE && a.pass_kind == 1) upd_merge_tile(a, h, tile, sh, dyn);
+    if (uni(sh.st.kind == SK_MERGE) && a.pass_kind == 1) upd_merge_tile(a, h, tile, sh, dyn, pre, spec);
+    __syncthreads();  // every read of the head's shared data is done
+    if (tid == 0) ticket = arrive_take(a, h, tile);
   } else {
-    upd_token_tile(a, sh, h, tile);
+    upd_token_tile(a, sh, h, tile, ticket);
   }
 
-  // Arrival, after a barrier that follows every read of the head's shared
-  // data.  Tile i counts on sub-counter i % kArriveFan; the last arrival
-  // of each sub-counter counts on the head counter, and the last of those
-  // is the head's last workgroup.  Each counter sits on its own 128-byte
-  // line, so arrivals at one address stay few.
+  if (tid == 0) sh.last = arrive_last(a, h, merge_tile ? tile : a.n_merge + tile, ticket);
   __syncthreads();
-  if (tid == 0) {
-    const int n_tiles = a.n_merge + a.n_scat;
-    const int idx = merge_tile ? tile : a.n_merge + tile;
-    const int sub = idx % kArriveFan;
-    const int sub_n = n_tiles / kArriveFan + (sub < n_tiles % kArriveFan ? 1 : 0);
-    const int n_sub = min(kArriveFan, n_tiles);
-    int32_t *ctr = a.arrive + static_cast<int64_t>(h) * (kArriveFan + 1) * kArriveStride;
-    int32_t *hc = ctr + kArriveFan * kArriveStride;
-    int last = 0;
-    if (atomicAdd(ctr + sub * kArriveStride, 1) == sub_n - 1) {
-      atomicExch(ctr + sub * kArriveStride, 0);
-      last = atomicAdd(hc, 1) == n_sub - 1;
-      if (last) atomicExch(hc, 0);
-    }
-    sh.last = last;
-  }
-  __syncthreads();
-  if (!sh.last) return;
-  if (!sh.staged) upd_stage(a, sh, h);  // uniform
-  const bool merge_head = a.n_merge > 0 && a.pass_kind == 1 && sh.st.kind == SK_MERGE;
-  if (tid == 0) {
-    if (!sh.machine_done) {
+  if (!uni(sh.last)) return;
+  if (!uni(sh.staged)) upd_stage(a, sh, h);
+  const bool merge_head = a.n_merge > 0 && a.pass_kind == 1 && uni(sh.st.kind == SK_MERGE);
+  if (!uni(sh.machine_done)) {
+    if (tid == 0) {
       upd_machine(a, sh);
       if (merge_head) upd_merge_plan(a, h, sh);
     }
-    sh.r = upd_route(a, h);
+    __syncthreads();
   }
-  __syncthreads();
   if (a.pass_kind == 1 && tid < kStateWords)
     reinterpret_cast<uint32_t *>(a.states + h)[tid] = reinterpret_cast<const uint32_t *>(&sh.st)[tid];
   if (tid < 3) {
@@ -1621,7 +1779,7 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
     if (D / 8 > 64) return fail(PKV_ERR_UNSUPPORTED, "cache_update: merges need head_dim <= 512, got %d", D);
     const int gpt = merge_tile_groups(D);
     u.n_merge = (MTPA + gpt - 1) / gpt;
-    smem = static_cast<size_t>(tile_list_words(FSEQ, gpt)) * sizeof(int32_t);
+    smem = static_cast<size_t>(merge_lds_words(FSEQ, MMA)) * sizeof(int32_t);
     if (smem > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(update_kernel),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(smem)) != hipSuccess)
