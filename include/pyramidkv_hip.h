@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PKV_ABI_VERSION 1
+#define PKV_ABI_VERSION 2
 
 typedef void *pkv_stream_t; /* hipStream_t; NULL selects the null stream */
 
@@ -342,7 +342,7 @@ typedef struct pkv_update_args {
   int32_t pass_kind;         /* 0 noisy, 1 clean */
   int32_t shift_pending;     /* 1: this block's recent shift is already in the pool */
   int32_t spatial_width;     /* W of the (y, x) = (tok / W, tok % W) grid */
-  int32_t has_merge_head;    /* the layer has a Veil head: clean passes accumulate merges */
+  int32_t reserved;          /* 0 */
   const uint16_t *new_k;     /* [L_in, H, D] rows, token stride tok_stride */
   const uint16_t *new_v;
   int64_t tok_stride;        /* elements between consecutive tokens (H*D) */
@@ -351,6 +351,8 @@ typedef struct pkv_update_args {
   const int64_t *sink_caps_layer; /* [H] */
   int64_t *committed_vc_layer;    /* [H,3] */
   void *workspace;           /* pkv_cache_update_workspace_size bytes */
+  uint64_t merge_heads;      /* bit h: head h is a Veil head, whose clean passes accumulate
+                                merges (bit 63 stands for every head >= 63); 0: none */
 } pkv_update_args;
 
 /* MegaCache.update of one layer (_mega_cache.py:136-414) in one launch:

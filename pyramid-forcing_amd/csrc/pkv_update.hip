@@ -899,7 +899,10 @@ struct UpdArgs {
   uint32_t src_fb, src_hb, src_tb;
   int64_t t0;
   int layer, H, F, FSEQ, D, width, max_sink, max_middle, max_recent, MMA, MMB, MTPA;
-  int pass_kind, shift_pending, n_merge, n_scat;
+  int pass_kind, shift_pending;
+  int n_merge, n_scat;  // merge tiles per merge head (0: no merges this call), token tiles per head
+  int n_mh;             // merge heads
+  uint64_t merge_heads; // bit h (bit 63 for every head >= 63): h is a merge head
 };
 
 struct UpdShared {
@@ -1022,7 +1025,8 @@ __host__ __device__ inline int64_t merge_lds_words(int FSEQ, int MMA) {
 // qualify (then nothing is loaded); frames whose lists turn out otherwise
 // load their members themselves.
 constexpr int kPreFrames = 3;
-constexpr int kPreTok = 4;
+constexpr int kPrePatch = 2;  // the Veil patch of the shipped policy
+constexpr int kPreTok = kPrePatch * kPrePatch;
 struct MergePre {
   uint4 x[kPreFrames][kPreTok];
 };
@@ -1042,12 +1046,11 @@ struct MergeLane {
 };
 
 __device__ __forceinline__ int merge_prefetch(const UpdArgs &a, int h, int mt, MergePre &pre) {
-  const int p = ld_uniform(&a.states[h].patch_size);
-  const int kind = ld_uniform(&a.states[h].kind);
+  // the patch size is assumed to be kPrePatch, so that the loads depend on
+  // nothing the kernel reads; the tile drops them for any other patch
+  constexpr int p = kPrePatch;
   const int FSEQ = a.FSEQ, W = min(a.width, FSEQ);
-  if (kind != SK_MERGE || a.F > kPreFrames || p <= 0 || p * p > kPreTok || FSEQ % W != 0 || W % p != 0 ||
-      (FSEQ / W) % p != 0)
-    return 0;
+  if (a.F > kPreFrames || FSEQ % W != 0 || W % p != 0 || (FSEQ / W) % p != 0) return 0;
   const MergeLane ln(a, mt);
   if (ln.own && ln.g < FSEQ / (p * p)) {
     const uint16_t *src = ln.is_v ? a.src.v : a.src.k;
@@ -1069,18 +1072,24 @@ __device__ __forceinline__ int merge_prefetch(const UpdArgs &a, int h, int mt, M
 // the LDS writes)
 __device__ __forceinline__ void merge_stage(const UpdArgs &a, int h, const MergeLane &ln, int32_t *dyn) {
   const int tid = threadIdx.x, FSEQ = a.FSEQ, fw = merge_fseq_words(FSEQ);
-  const int n = a.MMA * FSEQ;
   const int32_t *gids = a.ml.accum_group_ids + static_cast<int64_t>(h) * a.MMA * FSEQ;
-  constexpr int kB = 8;
-  for (int i0 = 0; i0 < n; i0 += kB * kUpdThreads) {
-    int32_t v[kB];
+  if (FSEQ % 4 == 0) {  // 16-byte pieces (the slots' ids start 16-byte aligned)
+    const int per = FSEQ / 4, n = a.MMA * per;
+    const int4 *g4 = reinterpret_cast<const int4 *>(gids);
+    constexpr int kB = 4;
+    for (int i0 = 0; i0 < n; i0 += kB * kUpdThreads) {
+      int4 v[kB];
 #pragma unroll
-    for (int k = 0; k < kB; ++k) v[k] = gids[min(i0 + tid + k * kUpdThreads, n - 1)];
+      for (int k = 0; k < kB; ++k) v[k] = g4[min(i0 + tid + k * kUpdThreads, n - 1)];
 #pragma unroll
-    for (int k = 0; k < kB; ++k) {
-      const int i = i0 + tid + k * kUpdThreads;
-      if (i < n) dyn[fw + (i / FSEQ) * fw + i % FSEQ] = v[k];
+      for (int k = 0; k < kB; ++k) {
+        const int i = i0 + tid + k * kUpdThreads;
+        if (i < n) reinterpret_cast<int4 *>(dyn + fw + (i / per) * fw)[i % per] = v[k];
+      }
     }
+  } else {
+    const int n = a.MMA * FSEQ;
+    for (int i = tid; i < n; i += kUpdThreads) dyn[fw + (i / FSEQ) * fw + i % FSEQ] = gids[i];
   }
   if (kStageAccumulators && a.MMA <= kStagedSlots && ln.own) {
     const float *acc_sum = ln.is_v ? a.ml.accum_sum_v : a.ml.accum_sum_k;
@@ -1257,9 +1266,9 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
     }
     if (fin >= 0 && fin < a.MMB && mt == 0 && tid == 0) ml.merge_token_count[static_cast<int64_t>(h) * a.MMB + fin] = ng;
   };
-  // the prefetched chunks serve when every merge frame's lists are the
-  // closed form of width spec (uniform)
-  bool closed = spec != 0;
+  // the prefetched chunks serve when the patch is the prefetch's and every
+  // merge frame's lists are the closed form of width spec (uniform)
+  bool closed = spec != 0 && p == kPrePatch;
   for (int f = 0; f < a.F && closed; ++f)
     if (sh.f_src[f] != kSrcNone) closed = frame_width(f) == spec;
   if (uni(closed)) {
@@ -1282,12 +1291,24 @@ __device__ inline int32_t *arrive_counters(const UpdArgs &a, int h) {
   return a.arrive + static_cast<int64_t>(h) * (kArriveFan + 1) * kArriveStride;
 }
 
+// Whether head h's clean passes accumulate merges, and the i-th such head
+__device__ inline bool is_merge_head(const UpdArgs &a, int h) {
+  return a.n_merge > 0 && ((a.merge_heads >> (h < 63 ? h : 63)) & 1);
+}
+__device__ inline int merge_head_at(const UpdArgs &a, int i) {
+  uint64_t m = a.merge_heads & ~(uint64_t{1} << 63);
+  const int low = __popcll(m);
+  if (i >= low) return 63 + (i - low);
+  for (int k = 0; k < i; ++k) m &= m - 1;
+  return __builtin_ctzll(m);
+}
+
 __device__ inline int arrive_take(const UpdArgs &a, int h, int idx) {
   return atomicAdd(arrive_counters(a, h) + (idx % kArriveFan) * kArriveStride, 1);
 }
 
 __device__ inline int arrive_last(const UpdArgs &a, int h, int idx, int ticket) {
-  const int n_tiles = a.n_merge + a.n_scat;
+  const int n_tiles = (is_merge_head(a, h) ? a.n_merge : 0) + a.n_scat;
   const int sub = idx % kArriveFan;
   const int sub_n = n_tiles / kArriveFan + (sub < n_tiles % kArriveFan ? 1 : 0);
   if (ticket != sub_n - 1) return 0;
@@ -1307,9 +1328,9 @@ __device__ __forceinline__ void upd_stage(const UpdArgs &a, UpdShared &sh, int h
   const int64_t hs0 = static_cast<int64_t>(h) * a.MMA;
   if (tid < kStateWords) {
     reinterpret_cast<uint32_t *>(&sh.st)[tid] = reinterpret_cast<const uint32_t *>(a.states + h)[tid];
-  } else if (a.n_merge > 0 && tid < kStateWords + a.MMA) {
+  } else if (is_merge_head(a, h) && tid < kStateWords + a.MMA) {
     sh.g_ng[tid - kStateWords] = a.ml.accum_num_groups[hs0 + tid - kStateWords];
-  } else if (a.n_merge > 0 && tid < kStateWords + 2 * a.MMA) {
+  } else if (is_merge_head(a, h) && tid < kStateWords + 2 * a.MMA) {
     const int s = tid - kStateWords - a.MMA;
     sh.g_wsum[s] = a.ml.accum_weight_sum ? a.ml.accum_weight_sum[hs0 + s] : 0.0f;
   }
@@ -1375,7 +1396,7 @@ __device__ __forceinline__ void upd_token_tile(const UpdArgs &a, UpdShared &sh, 
   // counters) is done: arrive now, so that the head's write-back overlaps
   // the stores below
   __syncthreads();
-  if (tid == 0) ticket = arrive_take(a, h, a.n_merge + tile);
+  if (tid == 0) ticket = arrive_take(a, h, (is_merge_head(a, h) ? a.n_merge : 0) + tile);
   uint16_t *sink_k = pools.k[0] + lh * a.max_sink * slot_elems;
   uint16_t *sink_v = pools.v[0] + lh * a.max_sink * slot_elems;
   uint16_t *mid_k = pools.k[1] + lh * a.max_middle * slot_elems;
@@ -1478,14 +1499,15 @@ __device__ __forceinline__ void upd_token_tile(const UpdArgs &a, UpdShared &sh, 
 }
 
 __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
-  extern __shared__ int32_t dyn[];
+  extern __shared__ __attribute__((aligned(16))) int32_t dyn[];
   __shared__ __attribute__((aligned(16))) UpdShared sh;
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
   const int F = a.F, FSEQ = a.FSEQ;
-  const bool merge_tile = b < a.H * a.n_merge;
-  const int h = merge_tile ? b / a.n_merge : (b - a.H * a.n_merge) / a.n_scat;
-  const int tile = merge_tile ? b % a.n_merge : (b - a.H * a.n_merge) % a.n_scat;
+  const int n_mt = a.n_mh * a.n_merge;
+  const bool merge_tile = b < n_mt;
+  const int h = merge_tile ? merge_head_at(a, b / a.n_merge) : (b - n_mt) / a.n_scat;
+  const int tile = merge_tile ? b % a.n_merge : (b - n_mt) % a.n_scat;
   int ticket = 0;  // thread 0: the arrival sub-counter's previous value
   if (merge_tile) {
     const Route r = upd_route(a, h);
@@ -1510,11 +1532,11 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
     upd_token_tile(a, sh, h, tile, ticket);
   }
 
-  if (tid == 0) sh.last = arrive_last(a, h, merge_tile ? tile : a.n_merge + tile, ticket);
+  if (tid == 0) sh.last = arrive_last(a, h, merge_tile ? tile : (is_merge_head(a, h) ? a.n_merge : 0) + tile, ticket);
   __syncthreads();
   if (!uni(sh.last)) return;
   if (!uni(sh.staged)) upd_stage(a, sh, h);
-  const bool merge_head = a.n_merge > 0 && a.pass_kind == 1 && uni(sh.st.kind == SK_MERGE);
+  const bool merge_head = is_merge_head(a, h) && a.pass_kind == 1 && uni(sh.st.kind == SK_MERGE);
   if (!uni(sh.machine_done)) {
     if (tid == 0) {
       upd_machine(a, sh);
@@ -1728,7 +1750,11 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   if (D / 8 > kUpdThreads) return fail(PKV_ERR_UNSUPPORTED, "cache_update: head_dim %d exceeds %d", D, 8 * kUpdThreads);
   const int64_t l = a->layer;
   const int MMA = geo->max_merge_active, MMB = geo->max_merge_blocks, MTPA = geo->max_merge_tokens;
-  const bool merge = a->pass_kind == 1 && a->has_merge_head;
+  // merge heads: bit h of merge_heads, bit 63 standing for every head >= 63
+  uint64_t mh_mask = a->merge_heads;
+  if (H < 64) mh_mask &= (uint64_t{1} << H) - 1;
+  const int n_mh = __builtin_popcountll(mh_mask & ~(uint64_t{1} << 63)) + ((mh_mask >> 63) & 1 ? H - 63 : 0);
+  const bool merge = a->pass_kind == 1 && n_mh > 0;
   const int cpt = D / 8, per_tile = kUpdThreads / cpt;
   UpdArgs u;
   u.states = reinterpret_cast<HeadState *>(a->states_layer);
@@ -1768,6 +1794,8 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   u.pass_kind = a->pass_kind; u.shift_pending = a->shift_pending;
   u.n_scat = (FSEQ + per_tile - 1) / per_tile;
   u.n_merge = 0;
+  u.n_mh = merge ? n_mh : 0;
+  u.merge_heads = mh_mask;
   size_t smem = 0;
   if (merge) {
     if (FSEQ > kMaxMergeFseq)
@@ -1785,7 +1813,8 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
                                             static_cast<int>(smem)) != hipSuccess)
       return fail(PKV_ERR_HIP, "cache_update: cannot reserve %zu bytes of LDS", smem);
   }
-  hipLaunchKernelGGL(update_kernel, dim3(H * (u.n_merge + u.n_scat)), dim3(kUpdThreads), smem, as_stream(stream), u);
+  hipLaunchKernelGGL(update_kernel, dim3(u.n_mh * u.n_merge + H * u.n_scat), dim3(kUpdThreads), smem, as_stream(stream),
+                     u);
   return check_launch("update_kernel");
 }
 

@@ -681,7 +681,7 @@ static Tensor dit_gelu_tanh(Tensor x) {
 // Fused MegaCache.update for one layer (see pkv_cache_update).
 static void cache_update(Mgr mgr, Tensor states_layer, Tensor sink_caps_layer, Tensor committed_vc_layer,
                          Tensor new_k, Tensor new_v, int64_t layer, int64_t t0, int64_t pass_kind,
-                         int64_t shift_pending, int64_t spatial_width, bool has_merge_head) {
+                         int64_t shift_pending, int64_t spatial_width, int64_t merge_heads) {
   TORCH_CHECK(mgr.get() != nullptr, "cache_update: manager is null");
   mgr->require_bf16("cache_update");
   TORCH_CHECK(new_k.is_cuda() && new_k.scalar_type() == at::kBFloat16 && new_v.sizes() == new_k.sizes(),
@@ -714,7 +714,8 @@ static void cache_update(Mgr mgr, Tensor states_layer, Tensor sink_caps_layer, T
   a.pass_kind = static_cast<int32_t>(pass_kind);
   a.shift_pending = static_cast<int32_t>(shift_pending);
   a.spatial_width = static_cast<int32_t>(spatial_width);
-  a.has_merge_head = has_merge_head ? 1 : 0;
+  a.reserved = 0;
+  a.merge_heads = static_cast<uint64_t>(merge_heads);
   a.new_k = reinterpret_cast<const uint16_t *>(new_k.data_ptr());
   a.new_v = reinterpret_cast<const uint16_t *>(new_v.data_ptr());
   a.tok_stride = new_k.stride(1);
@@ -995,7 +996,7 @@ static Tensor dit_res_ln(Tensor x, Tensor, c10::optional<Tensor>, c10::optional<
   return at::empty(x.sizes(), x.options().dtype(at::kBFloat16));
 }
 static void cache_update(Mgr, Tensor, Tensor, Tensor, Tensor, Tensor, int64_t, int64_t, int64_t, int64_t, int64_t,
-                         bool) {}
+                         int64_t) {}
 static void scatter_copy(Tensor, Tensor, Tensor, Tensor, int64_t) {}
 static void pos_override(Tensor, Tensor, Tensor, Tensor) {}
 static void write_frames(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor) {}
@@ -1099,7 +1100,7 @@ TORCH_LIBRARY(adahead, m) {
         "float eps) -> Tensor");
   m.def("cache_update(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, Tensor(a!) states_layer, "
         "Tensor sink_caps_layer, Tensor(b!) committed_vc_layer, Tensor new_k, Tensor new_v, int layer, int t0, "
-        "int pass_kind, int shift_pending, int spatial_width, bool has_merge_head) -> ()");
+        "int pass_kind, int shift_pending, int spatial_width, int merge_heads) -> ()");
   m.def("update_descriptors(__torch__.torch.classes.adahead.PyramidKVCacheManager mgr, int frames) -> Tensor[]");
   m.def("scatter_copy(Tensor src_ptrs, Tensor lengths, Tensor offsets, Tensor(a!) dst, int col_dim) -> ()");
   m.def("apply_pos_override(Tensor(a!) pos, Tensor starts, Tensor ends, Tensor vals) -> ()");

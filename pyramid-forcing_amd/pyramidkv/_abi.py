@@ -75,10 +75,10 @@ class AttnArgs(ctypes.Structure):
 
 class UpdateArgs(ctypes.Structure):
     _fields_ = [("layer", _c_i32), ("frames", _c_i32), ("t0", _c_i64), ("pass_kind", _c_i32),
-                ("shift_pending", _c_i32), ("spatial_width", _c_i32), ("has_merge_head", _c_i32),
+                ("shift_pending", _c_i32), ("spatial_width", _c_i32), ("reserved", _c_i32),
                 ("new_k", _c_p), ("new_v", _c_p), ("tok_stride", _c_i64), ("head_stride", _c_i64),
                 ("states_layer", _c_p), ("sink_caps_layer", _c_p), ("committed_vc_layer", _c_p),
-                ("workspace", _c_p)]
+                ("workspace", _c_p), ("merge_heads", ctypes.c_uint64)]
 
 
 _lib = None

@@ -52,6 +52,7 @@ class MegaCacheCtx:
     has_merge_head: bool = False
     # per layer: any Veil (merge) head; layers without one skip the merge launches
     layer_has_merge: list = field(default_factory=list)
+    layer_merge_heads: list = field(default_factory=list)  # per layer: bit h set for each Veil head h
     sink_caps_per_head: torch.Tensor = None
     committed_vc: torch.Tensor = None
     freqs: torch.Tensor = None
@@ -110,7 +111,7 @@ class MegaCache:
             nk = nk.contiguous()
         _ops.ops().cache_update(ctx.mgr, ctx.states_bytes[l], ctx.sink_caps_per_head[l], ctx.committed_vc[l], nk, nv,
                                 l, t0, 1 if clean else 0, 1 if pending == t0 else 0, ctx.spatial_width,
-                                bool(ctx.layer_has_merge[l] if ctx.layer_has_merge else ctx.has_merge_head))
+                                ctx.layer_merge_heads[l])
         ctx.pending_block[l] = None if clean else t0
 
     def last_update_descriptors(self, frames: int):
@@ -218,6 +219,16 @@ def _composition_to_perhead_state(composition: HeadComposition) -> ref.PerHeadSt
     return s
 
 
+def merge_head_mask(is_merge) -> int:
+    """Bit mask of the Veil heads of one layer, as the cache update takes it:
+    bit h for head h < 63, bit 63 for any head >= 63 (a signed int64)."""
+    m = 0
+    for h, v in enumerate(is_merge):
+        if v:
+            m |= 1 << min(h, 63)
+    return m - (1 << 64) if m >= 1 << 63 else m
+
+
 def build_mega_caches(num_layers: int, num_heads: int, head_dim: int, frame_seqlen: int, max_sink_frames: int,
                       max_middle_frames: int, max_recent_frames: int,
                       compositions: Sequence[Sequence[HeadComposition]], *, max_attend_chunks: int = 8,
@@ -238,12 +249,14 @@ def build_mega_caches(num_layers: int, num_heads: int, head_dim: int, frame_seql
     sink_caps = np.zeros((num_layers, num_heads), dtype=np.int64)
     any_merge = False
     layer_merge = []
+    layer_heads = []
     for l in range(num_layers):
         if len(compositions[l]) != num_heads:
             raise ValueError(f"compositions[{l}] has {len(compositions[l])} heads, expected {num_heads}")
         per_head = [_composition_to_perhead_state(c) for c in compositions[l]]
         layer_merge.append(any(s.kind == ref.SK_MERGE for s in per_head))
         any_merge = any_merge or layer_merge[-1]
+        layer_heads.append(merge_head_mask([s.kind == ref.SK_MERGE for s in per_head]))
         for h, s in enumerate(per_head):
             sink_caps[l, h] = int(s.sink_capacity)
         states_np[l] = _mega_state_ops.pack_states(per_head)
@@ -263,6 +276,7 @@ def build_mega_caches(num_layers: int, num_heads: int, head_dim: int, frame_seql
                        history_relative_t_max=history_relative_t_max,
                        history_time_soft_factor=history_time_soft_factor, spatial_width=spatial_width,
                        spatial_height=spatial_height, has_merge_head=any_merge, layer_has_merge=layer_merge,
+                       layer_merge_heads=layer_heads,
                        sink_caps_per_head=torch.from_numpy(sink_caps).to(device=device).contiguous(), freqs=freqs,
                        freq_parts=freq_parts, freq_parts_flat=freq_parts_flat,
                        pending_block=[None] * num_layers)
