@@ -1007,15 +1007,11 @@ __device__ int stored_grid_width(const int32_t *gids, int FSEQ, int W, int p, in
 __host__ __device__ inline int merge_tile_groups(int D) { return (kUpdThreads / 128) * (64 / (D / 8)); }
 
 // Dynamic LDS of a merge tile (int32 words): the group ids its scan reads
-// [FSEQ], the stored group ids of every accumulator slot [MMA][FSEQ] and,
-// with at most kStagedSlots slots, the accumulators this tile's threads own
-// [MMA][kUpdThreads][8] (fp32); each region starts on a 16-byte boundary.
-constexpr int kStagedSlots = 2;
-constexpr bool kStageAccumulators = false;
+// [FSEQ] and the stored group ids of every accumulator slot [MMA][FSEQ],
+// each region starting on a 16-byte boundary.
 __host__ __device__ inline int merge_fseq_words(int FSEQ) { return (FSEQ + 3) & ~3; }
 __host__ __device__ inline int64_t merge_lds_words(int FSEQ, int MMA) {
-  const int64_t fw = merge_fseq_words(FSEQ);
-  return fw * (1 + MMA) + (MMA <= kStagedSlots ? static_cast<int64_t>(MMA) * kUpdThreads * 8 : 0);
+  return static_cast<int64_t>(merge_fseq_words(FSEQ)) * (1 + MMA);
 }
 
 // Patch chunks of a merge tile's groups in every frame of a call, loaded
@@ -1050,8 +1046,8 @@ __device__ __forceinline__ int merge_prefetch(const UpdArgs &a, int h, int mt, M
   // nothing the kernel reads; the tile drops them for any other patch
   constexpr int p = kPrePatch;
   const int FSEQ = a.FSEQ, W = min(a.width, FSEQ);
-  if (a.F > kPreFrames || FSEQ % W != 0 || W % p != 0 || (FSEQ / W) % p != 0) return 0;
   const MergeLane ln(a, mt);
+  if (a.F > kPreFrames || FSEQ % W != 0 || W % p != 0 || (FSEQ / W) % p != 0) return 0;
   if (ln.own && ln.g < FSEQ / (p * p)) {
     const uint16_t *src = ln.is_v ? a.src.v : a.src.k;
     const int gcols = W / p;
@@ -1066,11 +1062,10 @@ __device__ __forceinline__ int merge_prefetch(const UpdArgs &a, int h, int mt, M
   return W;
 }
 
-// Merge tiles stage the stored group ids of every slot and, with at most
-// kStagedSlots slots, their threads' accumulators into LDS with the record
-// (one round trip for everything a tile reads; upd_stage's barrier orders
-// the LDS writes)
-__device__ __forceinline__ void merge_stage(const UpdArgs &a, int h, const MergeLane &ln, int32_t *dyn) {
+// Merge tiles stage the stored group ids of every slot into LDS with the
+// record (one round trip for what the tile reads before its frames;
+// upd_stage's barrier orders the LDS writes)
+__device__ __forceinline__ void merge_stage(const UpdArgs &a, int h, int32_t *dyn) {
   const int tid = threadIdx.x, FSEQ = a.FSEQ, fw = merge_fseq_words(FSEQ);
   const int32_t *gids = a.ml.accum_group_ids + static_cast<int64_t>(h) * a.MMA * FSEQ;
   if (FSEQ % 4 == 0) {  // 16-byte pieces (the slots' ids start 16-byte aligned)
@@ -1091,25 +1086,6 @@ __device__ __forceinline__ void merge_stage(const UpdArgs &a, int h, const Merge
     const int n = a.MMA * FSEQ;
     for (int i = tid; i < n; i += kUpdThreads) dyn[fw + (i / FSEQ) * fw + i % FSEQ] = gids[i];
   }
-  if (kStageAccumulators && a.MMA <= kStagedSlots && ln.own) {
-    const float *acc_sum = ln.is_v ? a.ml.accum_sum_v : a.ml.accum_sum_k;
-    float4 *accl = reinterpret_cast<float4 *>(dyn + fw * (1 + a.MMA));
-    float4 x[kStagedSlots][2];
-#pragma unroll
-    for (int s = 0; s < kStagedSlots; ++s)
-      if (s < a.MMA) {
-        const float4 *src = reinterpret_cast<const float4 *>(
-            acc_sum + ((static_cast<int64_t>(h) * a.MMA + s) * a.MTPA + ln.g) * a.D + ln.c);
-        x[s][0] = src[0];
-        x[s][1] = src[1];
-      }
-#pragma unroll
-    for (int s = 0; s < kStagedSlots; ++s)
-      if (s < a.MMA) {
-        accl[(s * kUpdThreads + tid) * 2] = x[s][0];
-        accl[(s * kUpdThreads + tid) * 2 + 1] = x[s][1];
-      }
-  }
 }
 
 __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, int32_t *dyn, const MergePre &pre,
@@ -1126,7 +1102,6 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
   uint16_t *merge_out = ln.is_v ? ml.merge_v : ml.merge_k;
   float ax[8];
   int cur = -1;
-  uint32_t touched = 0;    // slots whose accumulators this call has moved
   int ids_src = kSrcNone;  // source of the group ids the scan reads
   auto store_acc = [&](int slot) {
     const int64_t o = ((static_cast<int64_t>(h) * a.MMA + slot) * MTPA + g) * D + c;
@@ -1184,16 +1159,9 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
         if (cur >= 0) store_acc(cur);
         cur = slot;
         if (!is_new) {
-          if (kStageAccumulators && a.MMA <= kStagedSlots && !((touched >> slot) & 1)) {  // as staged
-            const float *accl = reinterpret_cast<const float *>(dyn + merge_fseq_words(FSEQ) * (1 + a.MMA)) +
-                                (slot * kUpdThreads + tid) * 8;
-            for (int e = 0; e < 8; ++e) ax[e] = accl[e];
-          } else {
-            const int64_t o = (hs * MTPA + g) * D + c;
-            for (int e = 0; e < 8; ++e) ax[e] = acc_sum[o + e];
-          }
+          const int64_t o = (hs * MTPA + g) * D + c;
+          for (int e = 0; e < 8; ++e) ax[e] = acc_sum[o + e];
         }
-        touched |= 1u << slot;
       }
       if (is_new)
         for (int e = 0; e < 8; ++e) ax[e] = 0.0f;
@@ -1513,7 +1481,7 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
     const Route r = upd_route(a, h);
     MergePre pre;
     const int spec = a.pass_kind == 1 ? merge_prefetch(a, h, tile, pre) : 0;
-    merge_stage(a, h, MergeLane(a, tile), dyn);
+    merge_stage(a, h, dyn);
     upd_stage(a, sh, h);
     if (tid == 0) {
       sh.staged = 1;
