@@ -355,6 +355,23 @@ typedef struct pkv_update_args {
                                 merges (bit 63 stands for every head >= 63); 0: none */
 } pkv_update_args;
 
+/* Veil eviction in one launch: pkv_state_update (clean pass) of H records
+ * for the frames t_vals[0..F) followed by pkv_merge_accum of those frames
+ * at the grid positions (t_vals[f], tok / W, tok % W) -- the positions
+ * MegaCache.update gives its frames (_mega_cache.py:203-215) -- with
+ * optional frame weights.  Results equal the two calls in sequence on those
+ * positions; new_k/new_v are [F, H, FSEQ, D] bf16.  It has no counterpart
+ * in the reference, which evicts through mega_state_update
+ * (anchor_store_update.cu:257-269) and mega_merge_accum
+ * (mega_merge_accum.cu:52-340); it is for callers that evict frames
+ * outside MegaCache.update.  Arrival counters live in a static device
+ * array: calls that overlap on one device race. */
+int pkv_evict_merge(uint8_t *states, int32_t num_heads, int32_t frames, int32_t frame_seqlen, int32_t head_dim,
+                    int32_t max_merge_active, int32_t max_merge_blocks, int32_t max_merge_tokens,
+                    const int64_t *t_vals, const uint16_t *new_k, const uint16_t *new_v, int32_t spatial_width,
+                    const float *frame_weights, const pkv_state_desc *desc, const pkv_merge_layer *ml,
+                    pkv_stream_t stream);
+
 /* MegaCache.update of one layer (_mega_cache.py:136-414) in one launch:
  * sink / recent routing of the F new frames with the recent FIFO shift, the
  * state machine and middle-pool writes of a clean pass, the Veil merge

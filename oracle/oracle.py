@@ -236,15 +236,20 @@ def layer_offset_slot_global(sg, sk, layer, g: Geometry):
     return (sg + off[kind] * (sk >= 0)).astype(np.int32)
 
 
-def pack(pools: dict, g: Geometry, sk, sg, sl, dst, tremap=None, tables=None, capacity=None):
+def pack(pools: dict, g: Geometry, sk, sg, sl, dst, tremap=None, tables=None, capacity=None, out=None):
     """pyramidkv_pack.cu:28-185.  pools: dict of numpy arrays with keys
     sink_k/v/pos, middle_k/v/pos, recent_k/v/pos, merge_k/v/pos (bf16 as
-    uint16).  Returns (k_out, v_out, pos_out)."""
+    uint16).  Returns (k_out, v_out, pos_out); out: those three arrays to
+    write into instead (segments write only their own rows, so disjoint
+    segment sets may pack into one output concurrently)."""
     cap = g.max_pack_tokens if capacity is None else capacity
     D = g.head_dim
-    k_out = np.zeros((cap, D), np.uint16)
-    v_out = np.zeros((cap, D), np.uint16)
-    pos_out = np.zeros((cap, 3), np.int64)
+    if out is not None:
+        k_out, v_out, pos_out = out
+    else:
+        k_out = np.zeros((cap, D), np.uint16)
+        v_out = np.zeros((cap, D), np.uint16)
+        pos_out = np.zeros((cap, 3), np.int64)
     names = ["sink", "middle", "recent", "merge"]
     pk = (ctypes.c_void_p * 4)(*[_p(pools[n + "_k"]).value for n in names])
     pv = (ctypes.c_void_p * 4)(*[_p(pools[n + "_v"]).value for n in names])

@@ -898,6 +898,9 @@ struct UpdArgs {
   // them and into one head's pools is below 2^31
   uint32_t src_fb, src_hb, src_tb;
   int64_t t0;
+  const int64_t *t_vals;  // [F] frame times, or null: t0 + f
+  const float *weights;   // [F] frame weights, or null: 1 (the reference's unweighted merge)
+  int counters;           // 1: route the frames and commit the counters; 0: records and merges only
   int layer, H, F, FSEQ, D, width, max_sink, max_middle, max_recent, MMA, MMB, MTPA;
   int pass_kind, shift_pending;
   int n_merge, n_scat;  // merge tiles per merge head (0: no merges this call), token tiles per head
@@ -912,6 +915,9 @@ struct UpdShared {
   int32_t staged, machine_done, last;
   int32_t g_ng[kMaxMergeSlots];  // stored group counts and weight sums of the slots
   float g_wsum[kMaxMergeSlots];
+  int64_t f_t[kUpdMaxFrames];    // frame times and weights
+  float f_w[kUpdMaxFrames];
+  float f_wsum[kUpdMaxFrames];   // the block's weight sum after frame f
   // merge bookkeeping: per frame, the list source and group count of its
   // block; per slot, the source, group count and weight sum after the call
   // and the stored-id check (-1 not done, 0 not the regular grid, else its
@@ -939,13 +945,13 @@ __device__ inline int32_t grid_gid(int t, int W, int p, int cols, int ng) {
 // (anchor_store_update.cu:257-269; noisy passes emit SKIP)
 __device__ void upd_machine(const UpdArgs &a, UpdShared &sh) {
   for (int f = 0; f < a.F; ++f)
-    sh.desc[f] = a.pass_kind == 1 ? sm_step(sh.st, static_cast<int32_t>(a.t0 + f)) : skip_desc();
+    sh.desc[f] = a.pass_kind == 1 ? sm_step(sh.st, static_cast<int32_t>(sh.f_t[f])) : skip_desc();
   sh.machine_done = 1;
 }
 
 // thread 0, after upd_machine on a Veil head: where each merge frame's
 // group lists come from, and every touched slot's group count and running
-// weight sum (one per frame: cache updates are unweighted)
+// weight sum (1 per frame without weights)
 __device__ void upd_merge_plan(const UpdArgs &a, int h, UpdShared &sh) {
   const int p = sh.st.patch_size, FSEQ = a.FSEQ, W = a.width, MTPA = a.MTPA;
   const int maxx = min(W, FSEQ) - 1, maxy = (FSEQ - 1) / W;
@@ -966,7 +972,7 @@ __device__ void upd_merge_plan(const UpdArgs &a, int h, UpdShared &sh) {
     if (d.is_new_block) {
       sh.s_src[s] = kSrcGrid;
       sh.s_ng[s] = sh.grid_ng;
-      sh.s_tpos[s] = a.t0 + f;
+      sh.s_tpos[s] = sh.f_t[f];
       sh.s_wsum[s] = 0.0f;
     } else if (sh.s_src[s] == kSrcNone) {
       sh.s_src[s] = s;
@@ -974,7 +980,8 @@ __device__ void upd_merge_plan(const UpdArgs &a, int h, UpdShared &sh) {
       sh.s_tpos[s] = 0;
       sh.s_wsum[s] = sh.g_wsum[s];
     }
-    sh.s_wsum[s] += 1.0f;
+    sh.s_wsum[s] += sh.f_w[f];
+    sh.f_wsum[f] = sh.s_wsum[s];
     sh.f_src[f] = sh.s_src[s];
     sh.f_ng[f] = sh.s_ng[s];
     sh.f_tpos[f] = sh.s_tpos[s];
@@ -1108,12 +1115,15 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
     for (int e = 0; e < 8; ++e) acc_sum[o + e] = ax[e];
   };
   // one member chunk added to the accumulators (one fp32 add per element)
+  // (w * x in fp32, then one add: the weighted merge; w = 1 without weights
+  // leaves x unchanged, so the sums are the reference's)
+  float w = 1.0f;
   auto add16 = [&](const uint4 &x) {
     const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      ax[2 * e] += bf16_to_f32(static_cast<uint16_t>(xw[e] & 0xffff));
-      ax[2 * e + 1] += bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
+      ax[2 * e] += w * bf16_to_f32(static_cast<uint16_t>(xw[e] & 0xffff));
+      ax[2 * e + 1] += w * bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
     }
   };
   // Width of the regular grid whose closed-form lists frame f's block
@@ -1142,6 +1152,7 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
     const int slot = d.accum_slot, is_new = d.is_new_block, fin = d.finalize_idx;
     const int ng = sh.f_ng[f];
     const int64_t hs = static_cast<int64_t>(h) * a.MMA + slot;
+    w = sh.f_w[f];
     int W = spec;
     if constexpr (!kClosed) {
       W = frame_width(f);
@@ -1207,7 +1218,8 @@ __device__ void upd_merge_tile(const UpdArgs &a, int h, int mt, UpdShared &sh, i
         }
       }
       if (fin >= 0 && fin < a.MMB && g < ng) {
-        const float div = static_cast<float>(cnt) * static_cast<float>(bf);
+        // count * sum(w) for weighted merges, else the reference's count * block_frames
+        const float div = static_cast<float>(cnt) * (a.weights ? sh.f_wsum[f] : static_cast<float>(bf));
         const float inv = div > 0.0f ? 1.0f / div : 0.0f;
         const int64_t hp = static_cast<int64_t>(h) * a.MMB + fin;
         uint4 ox;
@@ -1292,15 +1304,22 @@ __device__ inline int arrive_last(const UpdArgs &a, int h, int idx, int ticket) 
 __device__ __forceinline__ void upd_stage(const UpdArgs &a, UpdShared &sh, int h) {
   // with the record, on a clean pass of a layer with merges, the stored
   // group counts and weight sums of h's accumulator slots: one round trip
+  // and the call's frame times and weights
   const int tid = threadIdx.x;
   const int64_t hs0 = static_cast<int64_t>(h) * a.MMA;
+  constexpr int kNg = kStateWords, kWs = kNg + kMaxMergeSlots, kFr = kWs + kMaxMergeSlots;
+  static_assert(kFr + kUpdMaxFrames <= kUpdThreads, "one staged value per thread");
   if (tid < kStateWords) {
     reinterpret_cast<uint32_t *>(&sh.st)[tid] = reinterpret_cast<const uint32_t *>(a.states + h)[tid];
-  } else if (is_merge_head(a, h) && tid < kStateWords + a.MMA) {
-    sh.g_ng[tid - kStateWords] = a.ml.accum_num_groups[hs0 + tid - kStateWords];
-  } else if (is_merge_head(a, h) && tid < kStateWords + 2 * a.MMA) {
-    const int s = tid - kStateWords - a.MMA;
-    sh.g_wsum[s] = a.ml.accum_weight_sum ? a.ml.accum_weight_sum[hs0 + s] : 0.0f;
+  } else if (tid < kWs) {
+    if (is_merge_head(a, h) && tid - kNg < a.MMA) sh.g_ng[tid - kNg] = a.ml.accum_num_groups[hs0 + tid - kNg];
+  } else if (tid < kFr) {
+    const int s = tid - kWs;
+    if (is_merge_head(a, h) && s < a.MMA) sh.g_wsum[s] = a.ml.accum_weight_sum ? a.ml.accum_weight_sum[hs0 + s] : 0.0f;
+  } else if (tid < kFr + a.F) {
+    const int f = tid - kFr;
+    sh.f_t[f] = a.t_vals ? a.t_vals[f] : a.t0 + f;
+    sh.f_w[f] = a.weights ? a.weights[f] : 1.0f;
   }
   __syncthreads();
 }
@@ -1478,7 +1497,8 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
   const int tile = merge_tile ? b % a.n_merge : (b - n_mt) % a.n_scat;
   int ticket = 0;  // thread 0: the arrival sub-counter's previous value
   if (merge_tile) {
-    const Route r = upd_route(a, h);
+    Route r{};
+    if (a.counters) r = upd_route(a, h);
     MergePre pre;
     const int spec = a.pass_kind == 1 ? merge_prefetch(a, h, tile, pre) : 0;
     merge_stage(a, h, dyn);
@@ -1514,7 +1534,7 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
   }
   if (a.pass_kind == 1 && tid < kStateWords)
     reinterpret_cast<uint32_t *>(a.states + h)[tid] = reinterpret_cast<const uint32_t *>(&sh.st)[tid];
-  if (tid < 3) {
+  if (a.counters && tid < 3) {
     a.vc[h * 3 + tid] = sh.r.vc_post[tid];
     if (a.pass_kind == 1) a.committed_vc[h * 3 + tid] = sh.r.vc_post[tid];
   }
@@ -1564,6 +1584,33 @@ static int merge_scratch_device_ptr(void **out) {
       return fail(PKV_ERR_HIP, "merge_accum_static: hipGetSymbolAddress(scratch) on device %d: %s", dev,
                   hipGetErrorString(e));
     dev_ptr[dev] = p;
+  }
+  *out = dev_ptr[dev];
+  return PKV_OK;
+}
+
+// Arrival counters of pkv_evict_merge (the caller passes no workspace): a
+// file-scope device array, zero at load and left zero by every call, each
+// device holding its own copy; host code uses only the address that
+// hipGetSymbolAddress returns for the current device, looked up once per
+// device.  Calls that overlap on one device (two streams) race on it.
+constexpr int kEvictMaxHeads = 64;
+static __device__ __align__(256) int32_t evict_arrive[kEvictMaxHeads * (kArriveFan + 1) * kArriveStride];
+
+static int evict_arrive_ptr(int32_t **out) {
+  static std::mutex mu;
+  static int32_t *dev_ptr[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(PKV_ERR_HIP, "evict_merge: no current device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!dev_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(evict_arrive));
+    if (e != hipSuccess)
+      return fail(PKV_ERR_HIP, "evict_merge: hipGetSymbolAddress of the arrival counters failed: %s",
+                  hipGetErrorString(e));
+    dev_ptr[dev] = static_cast<int32_t *>(p);
   }
   *out = dev_ptr[dev];
   return PKV_OK;
@@ -1756,6 +1803,9 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   u.src_hb = static_cast<uint32_t>(a->head_stride * 2);
   u.src_tb = static_cast<uint32_t>(a->tok_stride * 2);
   u.t0 = a->t0;
+  u.t_vals = nullptr;
+  u.weights = nullptr;
+  u.counters = 1;
   u.layer = a->layer; u.H = H; u.F = F; u.FSEQ = FSEQ; u.D = D; u.width = a->spatial_width;
   u.max_sink = geo->max_sink; u.max_middle = geo->max_middle; u.max_recent = geo->max_recent;
   u.MMA = MMA; u.MMB = MMB; u.MTPA = MTPA;
@@ -1783,6 +1833,64 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   }
   hipLaunchKernelGGL(update_kernel, dim3(u.n_mh * u.n_merge + H * u.n_scat), dim3(kUpdThreads), smem, as_stream(stream),
                      u);
+  return check_launch("update_kernel");
+}
+
+int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t D, int32_t MMA, int32_t MMB,
+                    int32_t MTPA, const int64_t *t_vals, const uint16_t *new_k, const uint16_t *new_v,
+                    int32_t spatial_width, const float *frame_weights, const pkv_state_desc *desc,
+                    const pkv_merge_layer *ml, pkv_stream_t stream) {
+  if (H == 0 || F == 0) return PKV_OK;
+  if (!states || !t_vals || !new_k || !new_v || !desc || !ml || H < 0 || F < 0 || FSEQ <= 0 || D <= 0 || MMA <= 0 ||
+      MMB <= 0 || MTPA <= 0)
+    return fail(PKV_ERR_INVALID, "evict_merge: bad arguments");
+  if (!desc->dst_kind || !desc->dst_slot || !desc->src_frame || !desc->src_head || !desc->merge_accum_slot ||
+      !desc->merge_local_idx || !desc->merge_finalize_completed_idx || !desc->merge_is_new_block)
+    return fail(PKV_ERR_INVALID, "evict_merge: NULL descriptor array");
+  if (frame_weights && !ml->accum_weight_sum)
+    return fail(PKV_ERR_INVALID, "evict_merge: weighted merge needs accum_weight_sum");
+  if (spatial_width <= 0) return fail(PKV_ERR_INVALID, "evict_merge: spatial_width must be > 0");
+  if (H > kEvictMaxHeads) return fail(PKV_ERR_UNSUPPORTED, "evict_merge: %d heads exceed %d", H, kEvictMaxHeads);
+  if (F > kUpdMaxFrames) return fail(PKV_ERR_UNSUPPORTED, "evict_merge: %d frames exceed %d", F, kUpdMaxFrames);
+  if (D % 8 != 0 || D / 8 > 64)
+    return fail(PKV_ERR_UNSUPPORTED, "evict_merge: head_dim %d must be a multiple of 8, at most 512", D);
+  if (FSEQ > kMaxMergeFseq)
+    return fail(PKV_ERR_UNSUPPORTED, "evict_merge: frame_seqlen %d exceeds %d", FSEQ, kMaxMergeFseq);
+  if (MTPA > kMaxMergeGroups)
+    return fail(PKV_ERR_UNSUPPORTED, "evict_merge: %d tokens per anchor exceed %d", MTPA, kMaxMergeGroups);
+  if (MMA > kMaxMergeSlots)
+    return fail(PKV_ERR_UNSUPPORTED, "evict_merge: %d active merge blocks exceed %d", MMA, kMaxMergeSlots);
+  if (static_cast<int64_t>(F) * H * FSEQ * D * 2 >= (int64_t{1} << 31))
+    return fail(PKV_ERR_UNSUPPORTED, "evict_merge: the new frames exceed 2 GiB");
+  int32_t *arrive = nullptr;
+  int rc = evict_arrive_ptr(&arrive);
+  if (rc) return rc;
+  UpdArgs u{};
+  u.states = reinterpret_cast<HeadState *>(states);
+  u.src = FrameSrc{new_k, new_v, static_cast<int64_t>(H) * FSEQ * D, static_cast<int64_t>(FSEQ) * D, D};
+  u.ml = *ml;
+  u.desc = *desc;
+  u.arrive = arrive;
+  u.src_fb = static_cast<uint32_t>(static_cast<int64_t>(H) * FSEQ * D * 2);
+  u.src_hb = static_cast<uint32_t>(static_cast<int64_t>(FSEQ) * D * 2);
+  u.src_tb = static_cast<uint32_t>(D * 2);
+  u.t0 = 0;
+  u.t_vals = t_vals;
+  u.weights = frame_weights;
+  u.counters = 0;
+  u.H = H; u.F = F; u.FSEQ = FSEQ; u.D = D; u.width = spatial_width;
+  u.MMA = MMA; u.MMB = MMB; u.MTPA = MTPA;
+  u.pass_kind = 1;
+  u.n_scat = 0;
+  u.n_merge = (MTPA + merge_tile_groups(D) - 1) / merge_tile_groups(D);
+  u.n_mh = H;
+  u.merge_heads = H >= 64 ? ~uint64_t{0} : (uint64_t{1} << H) - 1;
+  const size_t smem = static_cast<size_t>(merge_lds_words(FSEQ, MMA)) * sizeof(int32_t);
+  if (smem > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(update_kernel),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          static_cast<int>(smem)) != hipSuccess)
+    return fail(PKV_ERR_HIP, "evict_merge: cannot reserve %zu bytes of LDS", smem);
+  hipLaunchKernelGGL(update_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u);
   return check_launch("update_kernel");
 }
 

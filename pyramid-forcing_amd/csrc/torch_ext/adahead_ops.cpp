@@ -523,6 +523,61 @@ static void mega_merge_accum_weighted(Tensor states, Tensor new_k, Tensor new_v,
              mpos, mtc, &frame_weights, &acc_wsum);
 }
 
+// Veil eviction in one launch (pkv_evict_merge): mega_state_update (clean
+// pass) then the (optionally weighted) merge accumulate of the frames at
+// the grid positions (t, tok / W, tok % W).
+static void mega_evict_merge(Tensor states, Tensor new_t_vals, Tensor new_k, Tensor new_v, int64_t spatial_width,
+                             c10::optional<Tensor> frame_weights, Tensor d0, Tensor d1, Tensor d2, Tensor d3,
+                             Tensor d4, Tensor d5, Tensor d6, Tensor d7, Tensor acc_k, Tensor acc_v, Tensor acc_pos,
+                             Tensor acc_gid, Tensor acc_tpg, Tensor acc_ng, Tensor acc_wsum, Tensor mk, Tensor mv,
+                             Tensor mpos, Tensor mtc) {
+  TORCH_CHECK(new_k.is_cuda() && new_k.dtype() == at::kBFloat16 && new_v.sizes() == new_k.sizes() &&
+                  new_v.dtype() == at::kBFloat16,
+              "mega_evict_merge: new_k/new_v must be CUDA bf16 of equal shape");
+  TORCH_CHECK(new_k.dim() == 4, "mega_evict_merge: new_k/new_v must be [F,H,FSEQ,D]");
+  const int64_t F = new_k.size(0), H = new_k.size(1), FSEQ = new_k.size(2), D = new_k.size(3);
+  TORCH_CHECK(new_t_vals.is_cuda() && new_t_vals.dtype() == at::kLong && new_t_vals.numel() == F,
+              "mega_evict_merge: new_t_vals must be CUDA int64 [F]");
+  TORCH_CHECK(states.is_cuda() && states.dtype() == at::kByte && states.is_contiguous() &&
+                  states.numel() >= H * pkv_perhead_state_size(),
+              "mega_evict_merge: states must hold H PerHeadState records");
+  for (const Tensor *t : {&d0, &d1, &d2, &d3, &d4, &d5, &d6, &d7})
+    TORCH_CHECK(t->dtype() == at::kInt && t->is_contiguous() && t->numel() >= H * F,
+                "mega_evict_merge: descriptor tensors must be contiguous int32 with H * F entries");
+  TORCH_CHECK(acc_k.dtype() == at::kFloat && acc_v.dtype() == at::kFloat && acc_tpg.dtype() == at::kFloat &&
+                  acc_wsum.dtype() == at::kFloat,
+              "mega_evict_merge: accumulators must be fp32");
+  TORCH_CHECK(mk.dtype() == at::kBFloat16 && mv.dtype() == at::kBFloat16, "mega_evict_merge: merge pools must be bf16");
+  for (const Tensor *t : {&acc_k, &acc_v, &acc_pos, &acc_gid, &acc_tpg, &acc_ng, &acc_wsum, &mk, &mv, &mpos, &mtc})
+    TORCH_CHECK(t->is_cuda() && t->is_contiguous() && t->size(0) == H,
+                "mega_evict_merge: accumulator / pool slices must be contiguous [H, ...] CUDA views of one layer");
+  TORCH_CHECK(acc_k.dim() == 4 && acc_k.size(3) == D && acc_gid.dim() == 3 && acc_gid.size(2) == FSEQ,
+              "mega_evict_merge: accumulators must be [H, MMA, MTPA, D] with group ids [H, MMA, FSEQ]");
+  const int64_t MMA = acc_k.size(1), MMB = mk.size(1), MTPA = acc_k.size(2);
+  if (H == 0 || F == 0) return;
+  auto nk = new_k.contiguous(), nv = new_v.contiguous();
+  auto tv = new_t_vals.contiguous();
+  Tensor w;
+  if (frame_weights) {
+    TORCH_CHECK(frame_weights->numel() == F, "mega_evict_merge: one weight per frame");
+    w = frame_weights->to(nk.device(), at::kFloat).contiguous();
+  }
+  pkv_state_desc desc{d0.data_ptr<int32_t>(), d1.data_ptr<int32_t>(), d2.data_ptr<int32_t>(),
+                      d3.data_ptr<int32_t>(), d4.data_ptr<int32_t>(), d5.data_ptr<int32_t>(),
+                      d6.data_ptr<int32_t>(), d7.data_ptr<int32_t>()};
+  pkv_merge_layer ml{acc_k.data_ptr<float>(), acc_v.data_ptr<float>(), acc_pos.data_ptr<int64_t>(),
+                     acc_gid.data_ptr<int32_t>(), acc_tpg.data_ptr<float>(), acc_ng.data_ptr<int32_t>(),
+                     acc_wsum.data_ptr<float>(), reinterpret_cast<uint16_t *>(mk.data_ptr()),
+                     reinterpret_cast<uint16_t *>(mv.data_ptr()), mpos.data_ptr<int64_t>(), mtc.data_ptr<int32_t>()};
+  pkv_check(pkv_evict_merge(states.data_ptr<uint8_t>(), static_cast<int32_t>(H), static_cast<int32_t>(F),
+                            static_cast<int32_t>(FSEQ), static_cast<int32_t>(D), static_cast<int32_t>(MMA),
+                            static_cast<int32_t>(MMB), static_cast<int32_t>(MTPA), tv.data_ptr<int64_t>(),
+                            reinterpret_cast<const uint16_t *>(nk.data_ptr()),
+                            reinterpret_cast<const uint16_t *>(nv.data_ptr()), static_cast<int32_t>(spatial_width),
+                            frame_weights ? w.data_ptr<float>() : nullptr, &desc, &ml, stream_for(nk)),
+            "mega_evict_merge");
+}
+
 // ---------------------------------------------------------------------------
 // ops added by this build
 // ---------------------------------------------------------------------------
@@ -1082,6 +1137,14 @@ TORCH_LIBRARY(adahead, m) {
         "Tensor(a!) accum_sum_k, Tensor(b!) accum_sum_v, Tensor(c!) accum_pos, Tensor(d!) accum_group_ids, "
         "Tensor(e!) accum_tokens_per_group, Tensor(f!) accum_num_groups, Tensor(g!) merge_k_pool, "
         "Tensor(h!) merge_v_pool, Tensor(i!) merge_pos_pool, Tensor(j!) merge_token_count) -> ()");
+  m.def("mega_evict_merge(Tensor(a!) states, Tensor new_t_vals, Tensor new_k, Tensor new_v, int spatial_width, "
+        "Tensor? frame_weights, Tensor(b!) desc_dst_kind, Tensor(c!) desc_dst_slot, Tensor(d!) desc_src_frame, "
+        "Tensor(e!) desc_src_head, Tensor(f!) desc_merge_accum_slot, Tensor(g!) desc_merge_local_idx, "
+        "Tensor(h!) desc_merge_finalize_completed_idx, Tensor(i!) desc_merge_is_new_block, Tensor(j!) accum_sum_k, "
+        "Tensor(k!) accum_sum_v, Tensor(l!) accum_pos, Tensor(m!) accum_group_ids, "
+        "Tensor(n!) accum_tokens_per_group, Tensor(o!) accum_num_groups, Tensor(p!) accum_weight_sum, "
+        "Tensor(q!) merge_k_pool, Tensor(r!) merge_v_pool, Tensor(s!) merge_pos_pool, "
+        "Tensor(t!) merge_token_count) -> ()");
   m.def("mega_merge_accum_weighted(Tensor states, Tensor new_k, Tensor new_v, Tensor new_pos, Tensor desc_dst_kind, "
         "Tensor desc_merge_accum_slot, Tensor desc_merge_finalize_completed_idx, Tensor desc_merge_is_new_block, "
         "Tensor frame_weights, Tensor(a!) accum_sum_k, Tensor(b!) accum_sum_v, Tensor(c!) accum_pos, "
@@ -1124,6 +1187,7 @@ TORCH_LIBRARY_IMPL(adahead, CUDA, m) {
   m.impl("mega_state_update", adahead::mega_state_update);
   m.impl("mega_merge_accum", adahead::mega_merge_accum);
   m.impl("mega_merge_accum_weighted", adahead::mega_merge_accum_weighted);
+  m.impl("mega_evict_merge", adahead::mega_evict_merge);
   m.impl("ragged_attention", adahead::ragged_attention);
   m.impl("rope_apply", adahead::rope_apply);
   m.impl("dit_layer_norm", adahead::dit_layer_norm);

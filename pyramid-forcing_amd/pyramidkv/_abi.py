@@ -100,6 +100,8 @@ def lib():
         L.pkv_merge_workspace_size.argtypes = [_c_i32] * 4
         L.pkv_merge_accum_static.argtypes = [_c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32] + \
             [_c_p] * 10
+        L.pkv_evict_merge.argtypes = [_c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p,
+                                      _c_i32, _c_p, _c_p, _c_p, _c_p]
         _lib = L
     return _lib
 

@@ -1,0 +1,91 @@
+"""mega_evict_merge (pkv_evict_merge): the state update of a clean pass and
+the (optionally weighted) Veil merge accumulate of the same frames in one
+launch, at the grid positions (t, tok / W, tok % W) that MegaCache.update
+gives its frames.  Driven over consecutive calls against the CPU oracle
+(oracle.state_update then oracle.merge_accum on those positions, the
+restatement of anchor_store_update.cu:43-269 and mega_merge_accum.cu:52-252):
+state records, descriptors, every accumulator (fp32 sums, group ids,
+counts, positions, weight sums) and the merge pools bit-exact after every
+call."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+if torch.cuda.is_available():
+    from gpu_util import DEV, to_dev, to_np
+    from pyramidkv import _ops
+
+pytestmark = pytest.mark.gpu
+
+D, MMA, MMB, MT = 128, 2, 6, 420
+
+
+def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None):
+    """kinds: per head 'merge' or 'cyclic' (default all 'merge')."""
+    rng = np.random.default_rng(seed)
+    kinds = kinds or ["merge"] * H
+    recs = [O.make_merge(2, int(rng.integers(2, 7))) if k == "merge" else O.make_cyclic(4, 2) for k in kinds]
+    states_host = O.states_to_bytes(recs)
+    states_dev = to_dev(states_host)
+    acc = dict(sum_k=np.zeros((H, MMA, MT, D), np.float32), sum_v=np.zeros((H, MMA, MT, D), np.float32),
+               pos=np.zeros((H, MMA, MT, 3), np.int64), gid=np.zeros((H, MMA, FSEQ), np.int32),
+               tpg=np.zeros((H, MMA, MT), np.float32), ng=np.zeros((H, MMA), np.int32),
+               wsum=np.zeros((H, MMA), np.float32), mk=np.zeros((H, MMB, MT, D), np.uint16),
+               mv=np.zeros((H, MMB, MT, D), np.uint16), mpos=np.zeros((H, MMB, MT, 3), np.int64),
+               mtc=np.zeros((H, MMB), np.int32))
+    dacc = {k: to_dev(v) for k, v in acc.items()}
+    ops = _ops.ops()
+    tok = np.arange(FSEQ)
+    for ci, t_vals in enumerate(calls):
+        F = len(t_vals)
+        print(f"evict_merge H={H} FSEQ={FSEQ} W={W} call {ci} t={t_vals} weighted={weighted}", flush=True)
+        nk = O.f32_to_bf16(rng.standard_normal((F, H, FSEQ, D)).astype(np.float32))
+        nv = O.f32_to_bf16(rng.standard_normal((F, H, FSEQ, D)).astype(np.float32))
+        pos = np.zeros((F, H, FSEQ, 3), np.int64)
+        pos[..., 0] = np.asarray(t_vals).reshape(F, 1, 1)
+        pos[..., 1] = tok // W
+        pos[..., 2] = tok % W
+        w = rng.uniform(0.1, 1.0, F).astype(np.float32) if weighted else None
+        desc = O.state_update(states_host, t_vals, 1)
+        dm = desc.copy()
+        dm[0] = np.where(desc[0] == O.DST_MERGE, desc[0], -1)
+        O.merge_accum(states_host, nk, nv, pos, dm, acc, w)
+        dd = [torch.full((H * F,), -7, dtype=torch.int32, device=DEV) for _ in range(8)]
+        ops.mega_evict_merge(states_dev, torch.tensor(t_vals, dtype=torch.int64, device=DEV),
+                             to_dev(nk).view(F, H, FSEQ, D), to_dev(nv).view(F, H, FSEQ, D), W,
+                             to_dev(w) if w is not None else None, *dd, dacc["sum_k"], dacc["sum_v"], dacc["pos"],
+                             dacc["gid"], dacc["tpg"], dacc["ng"], dacc["wsum"], dacc["mk"], dacc["mv"],
+                             dacc["mpos"], dacc["mtc"])
+        torch.cuda.synchronize()
+        assert np.array_equal(to_np(states_dev), states_host), f"call {ci}: state records differ"
+        for i in range(8):
+            assert np.array_equal(to_np(dd[i]), desc[i].astype(np.int32)), f"call {ci}: descriptor array {i} differs"
+        for k in acc:
+            got = to_np(dacc[k])
+            if not np.array_equal(got, acc[k]):
+                bad = np.argwhere(got != acc[k])
+                raise AssertionError(f"call {ci}: {k} differs at {len(bad)} places, first {bad[:4].tolist()}")
+
+
+def test_evict_single_frames_weighted_production_grid():
+    # the config-4 pattern: one 1,560-token frame per head and call
+    _evict_run(H=3, FSEQ=1560, W=52, calls=[[e + 1] for e in range(14)], seed=1, weighted=True)
+
+
+@pytest.mark.parametrize("F,weighted", [(3, False), (3, True), (4, False), (2, True)])
+def test_evict_multi_frame_calls_straddling_blocks(F, weighted):
+    calls = [[2 + F * b + f for f in range(F)] for b in range(24 // F)]
+    _evict_run(H=2, FSEQ=1560, W=52, calls=calls, seed=10 + F, weighted=weighted)
+
+
+def test_evict_irregular_grid_and_mixed_heads():
+    # 7-wide rows with a ragged last row and patch column (group ids scanned,
+    # not the closed form), 5 frames per call (a block finalizes and the next
+    # begins in one call), and a Wave head beside the Veil heads (state update
+    # only)
+    calls = [[5 * b + f for f in range(5)] for b in range(5)]
+    _evict_run(H=3, FSEQ=7 * 9 + 3, W=7, calls=calls, seed=2, weighted=True, kinds=["merge", "cyclic", "merge"])
