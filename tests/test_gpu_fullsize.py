@@ -14,9 +14,10 @@
   oracle's state machine and planner.  For three layers chosen to cover the
   label mixes, the oracle MegaCache model runs the whole rollout on the same
   data: pools and the packed K / V / positions bit-exact.
-* Config 4: 40 single-frame weighted Veil evictions of 12 heads through the
-  torch ops, bit-exact against the oracle (anchors, positions, counts and
-  the fp32 accumulators).
+* Config 4: 40 single-frame weighted Veil evictions of 12 heads, through the
+  reference's two ops and through the one-launch mega_evict_merge, both
+  bit-exact against the oracle (anchors, positions, counts and the fp32
+  accumulators).
 * Config 5: the causal DiT rollout in the Wan2.1-T2V-1.3B shape for 8
   chunks: finite outputs, and the caches advanced as the policy dictates
   (state records against the oracle state machine, valid counts and merge
@@ -196,6 +197,10 @@ def test_config4_weighted_evictions():
                mtc=np.zeros((H, MMB), np.int32))
     dacc = {n: to_dev(a) for n, a in acc.items()}
     desc = [torch.full((H,), -1, dtype=torch.int32, device=DEV) for _ in range(8)]
+    # the same evictions through the one-launch op (the bench's config-4 path)
+    sd1 = to_dev(states.copy())
+    dacc1 = {n: to_dev(a) for n, a in acc.items()}
+    desc1 = [torch.full((H,), -1, dtype=torch.int32, device=DEV) for _ in range(8)]
     tok = np.arange(FSEQ)
     for e in range(E):
         k = O.f32_to_bf16(rng.standard_normal((1, H, FSEQ, D)).astype(np.float32))
@@ -212,11 +217,19 @@ def test_config4_weighted_evictions():
                                       desc[0], desc[4], desc[6], desc[7], to_dev(w), dacc["sum_k"], dacc["sum_v"],
                                       dacc["pos"], dacc["gid"], dacc["tpg"], dacc["ng"], dacc["wsum"], dacc["mk"],
                                       dacc["mv"], dacc["mpos"], dacc["mtc"])
+        ops.mega_evict_merge(sd1, torch.tensor([e + 1], dtype=torch.int64, device=DEV), to_dev(k).view(torch.bfloat16),
+                             to_dev(v).view(torch.bfloat16), 52, to_dev(w), *desc1, dacc1["sum_k"], dacc1["sum_v"],
+                             dacc1["pos"], dacc1["gid"], dacc1["tpg"], dacc1["ng"], dacc1["wsum"], dacc1["mk"],
+                             dacc1["mv"], dacc1["mpos"], dacc1["mtc"])
     torch.cuda.synchronize()
     assert np.array_equal(to_np(sd), states)
+    assert np.array_equal(to_np(sd1), states), "mega_evict_merge: state records differ"
+    for i in range(8):
+        assert torch.equal(desc[i], desc1[i]), f"mega_evict_merge: descriptor array {i} differs"
     for n, a in acc.items():
-        got = to_np(dacc[n])
-        assert np.array_equal(got.view(a.dtype) if got.dtype != a.dtype else got, a), f"{n} differs"
+        for tag, dd in (("two ops", dacc), ("mega_evict_merge", dacc1)):
+            got = to_np(dd[n])
+            assert np.array_equal(got.view(a.dtype) if got.dtype != a.dtype else got, a), f"{tag}: {n} differs"
 
 
 def test_config5_full_shape_rollout():
