@@ -894,6 +894,7 @@ struct UpdArgs {
   pkv_merge_layer ml;  // this layer's merge pools
   pkv_state_desc desc;
   int32_t *arrive;     // [H]
+  int32_t *early;      // evict_kernel: per head, arrivals after the record reads (one 128-byte line each)
   // byte strides of the new frames (frame, head, token); every offset into
   // them and into one head's pools is below 2^31
   uint32_t src_fb, src_hb, src_tb;
@@ -1485,42 +1486,47 @@ __device__ __forceinline__ void upd_token_tile(const UpdArgs &a, UpdShared &sh, 
   }
 }
 
-__global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
-  extern __shared__ __attribute__((aligned(16))) int32_t dyn[];
-  __shared__ __attribute__((aligned(16))) UpdShared sh;
+// Merge tile `tile` of head h: record, stored group ids and the frames'
+// patch chunks loaded together, the state machine and merge bookkeeping on
+// thread 0, the tile's groups accumulated, then the arrival
+__device__ __forceinline__ void upd_merge_wg(const UpdArgs &a, UpdShared &sh, int32_t *dyn, int h, int tile,
+                                             int &ticket, int tiles = 1) {
   const int tid = threadIdx.x;
-  const int b = blockIdx.x;
-  const int F = a.F, FSEQ = a.FSEQ;
-  const int n_mt = a.n_mh * a.n_merge;
-  const bool merge_tile = b < n_mt;
-  const int h = merge_tile ? merge_head_at(a, b / a.n_merge) : (b - n_mt) / a.n_scat;
-  const int tile = merge_tile ? b % a.n_merge : (b - n_mt) % a.n_scat;
-  int ticket = 0;  // thread 0: the arrival sub-counter's previous value
-  if (merge_tile) {
-    Route r{};
-    if (a.counters) r = upd_route(a, h);
-    MergePre pre;
-    const int spec = a.pass_kind == 1 ? merge_prefetch(a, h, tile, pre) : 0;
-    merge_stage(a, h, dyn);
-    upd_stage(a, sh, h);
-    if (tid == 0) {
-      sh.staged = 1;
-      sh.machine_done = 0;
-      sh.r = r;
-      if (a.pass_kind == 1 && sh.st.kind == SK_MERGE) {
-        upd_machine(a, sh);
-        upd_merge_plan(a, h, sh);
-      }
+  Route r{};
+  if (a.counters) r = upd_route(a, h);
+  MergePre pre;
+  int spec = a.pass_kind == 1 ? merge_prefetch(a, h, tile * tiles, pre) : 0;
+  merge_stage(a, h, dyn);
+  upd_stage(a, sh, h);
+  if (tid == 0) {
+    sh.staged = 1;
+    sh.machine_done = 0;
+    sh.r = r;
+    if (a.pass_kind == 1 && sh.st.kind == SK_MERGE) {
+      upd_machine(a, sh);
+      upd_merge_plan(a, h, sh);
     }
-    __syncthreads();
-    if (uni(sh.st.kind == SK_MERGE) && a.pass_kind == 1) upd_merge_tile(a, h, tile, sh, dyn, pre, spec);
-    __syncthreads();  // every read of the head's shared data is done
-    if (tid == 0) ticket = arrive_take(a, h, tile);
-  } else {
-    upd_token_tile(a, sh, h, tile, ticket);
   }
+  __syncthreads();
+  if (uni(sh.st.kind == SK_MERGE) && a.pass_kind == 1) {
+    for (int j = 0; j < tiles; ++j) {  // merge tiles tile * tiles .. (several in an eviction workgroup)
+      const int mt = tile * tiles + j;
+      if (mt * merge_tile_groups(a.D) >= a.MTPA) break;
+      if (j > 0) spec = merge_prefetch(a, h, mt, pre);
+      upd_merge_tile(a, h, mt, sh, dyn, pre, spec);
+    }
+  }
+  __syncthreads();  // every read of the head's shared data is done
+  if (tid == 0) ticket = arrive_take(a, h, tile);
+}
 
-  if (tid == 0) sh.last = arrive_last(a, h, merge_tile ? tile : (is_merge_head(a, h) ? a.n_merge : 0) + tile, ticket);
+// Arrival index `idx` of head h resolved and, in the head's last
+// workgroup, the write-back: record, counters, descriptors and the merge
+// slots' group counts, weight sums and group ids
+__device__ __forceinline__ void upd_finish(const UpdArgs &a, UpdShared &sh, int h, int idx, int ticket) {
+  const int tid = threadIdx.x;
+  const int F = a.F, FSEQ = a.FSEQ;
+  if (tid == 0) sh.last = arrive_last(a, h, idx, ticket);
   __syncthreads();
   if (!uni(sh.last)) return;
   if (!uni(sh.staged)) upd_stage(a, sh, h);
@@ -1554,6 +1560,424 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
           a.ml.accum_group_ids[hs * FSEQ + t] = grid_gid(t, a.width, p, sh.grid_cols, sh.grid_ng);
     }
   }
+}
+
+__global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) int32_t dyn[];
+  __shared__ __attribute__((aligned(16))) UpdShared sh;
+  const int b = blockIdx.x;
+  const int n_mt = a.n_mh * a.n_merge;
+  const bool merge_tile = b < n_mt;
+  const int h = merge_tile ? merge_head_at(a, b / a.n_merge) : (b - n_mt) / a.n_scat;
+  const int tile = merge_tile ? b % a.n_merge : (b - n_mt) % a.n_scat;
+  int ticket = 0;  // thread 0: the arrival sub-counter's previous value
+  if (merge_tile)
+    upd_merge_wg(a, sh, dyn, h, tile, ticket);
+  else
+    upd_token_tile(a, sh, h, tile, ticket);
+  upd_finish(a, sh, h, merge_tile ? tile : (is_merge_head(a, h) ? a.n_merge : 0) + tile, ticket);
+}
+
+// ---- Veil eviction of one frame per call (pkv_evict_merge) ----------------
+//
+// A Veil step (anchor_store_update.cu:122-231) changes only the record's
+// last 39 words: the completed FIFO, the active blocks' ids, seen flags and
+// frame counts.  The step splits into a decision -- scalar arithmetic on
+// six of those words, the block frames and the capacity -- and its
+// application to the words, one word per lane of a wave (the FIFO shift
+// reads the next lane's word).  That replaces the state machine on one
+// thread over the LDS record, whose chain of dependent LDS accesses was the
+// longest step of an eviction.
+constexpr int kVeilWord0 = static_cast<int>(offsetof(HeadState, merge_completed_slot) / 4);
+constexpr int kVeilWords = kStateWords - kVeilWord0;
+constexpr int kVlCount = static_cast<int>(offsetof(HeadState, merge_completed_count) / 4) - kVeilWord0;
+constexpr int kVlId = static_cast<int>(offsetof(HeadState, merge_active_block_id) / 4) - kVeilWord0;
+constexpr int kVlSeen = static_cast<int>(offsetof(HeadState, merge_active_seen) / 4) - kVeilWord0;
+constexpr int kVlDone = static_cast<int>(offsetof(HeadState, merge_active_complete_count) / 4) - kVeilWord0;
+static_assert(kVeilWords <= 64, "one record word per lane");
+static_assert(kMaxMergeActive == 2 && kMaxMergeBlockFrames == 4, "one seen word per active block");
+static_assert(offsetof(HeadState, merge_completed_slot) % 4 == 0 && offsetof(HeadState, merge_completed_count) % 4 == 0 &&
+                  offsetof(HeadState, merge_active_seen) % 4 == 0 &&
+                  offsetof(HeadState, merge_active_complete_count) % 4 == 0,
+              "word-aligned Veil fields");
+static_assert(kVlCount == 5 * kMaxMergeBlocks, "the completed FIFO's five arrays precede its count");
+
+__device__ inline int32_t lane_word(uint32_t w, int l) {
+  return __builtin_amdgcn_readlane(static_cast<int>(w), l);
+}
+
+// The record words a Veil decision reads
+struct VeilWords {
+  uint32_t count;         // merge_completed_count (low byte)
+  int32_t id0, id1;       // merge_active_block_id
+  uint32_t seen0, seen1;  // merge_active_seen rows
+  uint32_t done;          // merge_active_complete_count (two low bytes)
+};
+
+// A decided Veil step: the frame's descriptor and the record's new values
+struct VeilStep {
+  FrameDesc d;
+  int32_t cap, shift, block_id, start, end, median, cc, id0, id1, done0, done1;
+  uint32_t seen0, seen1;
+  __device__ bool changes() const { return d.kind == PKV_DST_MERGE_ACCUM; }
+};
+
+// sm_merge's decision, with its parameter guards; a skipped frame (guards,
+// or a frame already seen) changes nothing
+__device__ inline VeilStep veil_decide(const VeilWords &v, int32_t bf, int32_t cap, int32_t t) {
+  VeilStep s;
+  s.d = skip_desc();
+  if (bf <= 0 || bf > kMaxMergeBlockFrames || cap <= 0 || cap > kMaxMergeBlocks || t < 0) return s;
+  const int32_t block_id = t / bf, local = t % bf;
+  int32_t id0 = v.id0, id1 = v.id1;
+  uint32_t seen0 = v.seen0, seen1 = v.seen1;
+  int32_t done0 = static_cast<int8_t>(v.done & 0xffu), done1 = static_cast<int8_t>((v.done >> 8) & 0xffu);
+  int32_t cc = static_cast<int8_t>(v.count & 0xffu);
+  int a = id0 == block_id ? 0 : (id1 == block_id ? 1 : -1);
+  int is_new = 0;
+  if (a < 0) {  // a free slot, else slot 0 is evicted; the slot taken is cleared
+    a = id0 == -1 ? 0 : (id1 == -1 ? 1 : 0);
+    is_new = 1;
+  }
+  int32_t id = a ? id1 : id0, done = a ? done1 : done0;
+  uint32_t seen = a ? seen1 : seen0;
+  if (is_new) {
+    id = block_id;
+    seen = 0;
+    done = 0;
+  }
+  if ((seen >> (8 * local)) & 0xffu) return s;  // a repeated frame leaves the record as it is
+  seen |= 1u << (8 * local);
+  done = static_cast<int8_t>(done + 1);
+  int32_t fin = -1;
+  s.shift = 0;
+  s.start = s.end = s.median = 0;
+  if (done >= bf) {  // the block completes into the FIFO
+    s.start = block_id * bf;
+    s.end = s.start + bf - 1;
+    s.median = (s.start + s.end) / 2;
+    s.shift = cc >= cap;
+    fin = s.shift ? cap - 1 : cc;
+    if (!s.shift) cc = static_cast<int8_t>(cc + 1);
+    id = -1;
+    seen = 0;
+    done = 0;
+  }
+  if (a) {
+    id1 = id;
+    seen1 = seen;
+    done1 = done;
+  } else {
+    id0 = id;
+    seen0 = seen;
+    done0 = done;
+  }
+  s.cap = cap;
+  s.block_id = block_id;
+  s.cc = cc;
+  s.id0 = id0;
+  s.id1 = id1;
+  s.seen0 = seen0;
+  s.seen1 = seen1;
+  s.done0 = done0;
+  s.done1 = done1;
+  s.d.kind = PKV_DST_MERGE_ACCUM;
+  s.d.slot = -1;
+  s.d.accum_slot = a;
+  s.d.local_idx = local;
+  s.d.finalize_idx = fin;
+  s.d.is_new_block = is_new;
+  return s;
+}
+
+// Record word kVeilWord0 + lane after the step (w: its value before, next:
+// the next lane's value before)
+__device__ inline uint32_t veil_apply(const VeilStep &s, uint32_t w, uint32_t next, int lane) {
+  if (!s.changes()) return w;
+  const int fin = s.d.finalize_idx;
+  uint32_t nw = w;
+  if (lane < kVlCount) {  // FIFO arrays: slot, block id, start, end, median
+    const int arr = lane / kMaxMergeBlocks, e = lane % kMaxMergeBlocks;
+    if (fin >= 0 && s.shift && e < s.cap - 1) nw = next;
+    if (fin >= 0 && e == fin)
+      nw = static_cast<uint32_t>(arr == 0 ? fin : arr == 1 ? s.block_id : arr == 2 ? s.start : arr == 3 ? s.end : s.median);
+  } else if (lane == kVlCount) {
+    nw = (w & ~0xffu) | (static_cast<uint32_t>(s.cc) & 0xffu);
+  } else if (lane == kVlId) {
+    nw = static_cast<uint32_t>(s.id0);
+  } else if (lane == kVlId + 1) {
+    nw = static_cast<uint32_t>(s.id1);
+  } else if (lane == kVlSeen) {
+    nw = s.seen0;
+  } else if (lane == kVlSeen + 1) {
+    nw = s.seen1;
+  } else if (lane == kVlDone) {
+    nw = (w & 0xffff0000u) | (static_cast<uint32_t>(s.done0) & 0xffu) | ((static_cast<uint32_t>(s.done1) & 0xffu) << 8);
+  }
+  return nw;
+}
+
+// The step applied in place to the words w held one per lane (lane l holds
+// word kVeilWord0 + l); called by whole waves
+__device__ inline void veil_apply_wave(const VeilStep &s, uint32_t &w) {
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  const uint32_t next = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((lane + 1) * 4, static_cast<int>(w)));
+  w = veil_apply(s, w, next, lane);
+}
+
+// Eviction workgroups cover kEvTiles of update_kernel's merge tiles (each
+// thread kEvTiles groups, same roles), so that the per-workgroup reads (the
+// record, the stored group ids) and the arrivals are fewer.
+constexpr int kEvTiles = 3;
+constexpr int kEvIdLoads = 2;  // 16-byte loads of stored group ids per thread
+constexpr int kEvMaxFseq = 4 * kEvIdLoads * kUpdThreads;
+__host__ __device__ inline int evict_tile_groups(int D) { return kEvTiles * merge_tile_groups(D); }
+
+// One frame per call.  One wave-wide gather brings the record's decision
+// words, the frame time and weight and the slots' counts while the frame's
+// patch chunks (regular grid of patch 2) stream in; the step is decided in
+// scalar registers, and only a continued block then reads its slot's sums,
+// stored group ids (verified against the grid by a block-wide vote) and
+// anchor positions.  A head this path does not cover (another strategy kind
+// or patch size, a continued block whose stored ids are not the grid's)
+// runs update_kernel's merge tiles instead; the choice is the same in every
+// workgroup of the head.  Launched only where the frame's grid of width
+// W = spatial width tiles into 2 x 2 patches with at most MTPA of them, with
+// at most 2 accumulator slots, FSEQ <= kEvMaxFseq, head_dim >= 32 and
+// 16-byte aligned frames, sums and group ids (pkv_evict_merge checks).
+__global__ void __launch_bounds__(kUpdThreads) evict_kernel(UpdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) int32_t dyn[];
+  __shared__ __attribute__((aligned(16))) UpdShared sh;
+  __shared__ uint32_t vote[kUpdThreads / 64];
+  constexpr int p = kPrePatch, kTok = kPreTok;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x / a.n_merge, tile = blockIdx.x % a.n_merge;
+  const int FSEQ = a.FSEQ, D = a.D, MTPA = a.MTPA, MMA = a.MMA, W = a.width;
+  const int cols = W / p, grid_ng = FSEQ / (p * p);
+  const int64_t hs0 = static_cast<int64_t>(h) * MMA;
+  const pkv_merge_layer &ml = a.ml;
+  const MergeLane ln0(a, tile * kEvTiles);
+  const int c = ln0.c, is_v = ln0.is_v;
+  int g[kEvTiles];
+  bool own[kEvTiles];
+#pragma unroll
+  for (int j = 0; j < kEvTiles; ++j) {
+    const MergeLane ln(a, tile * kEvTiles + j);
+    g[j] = ln.g;
+    own[j] = ln.own;
+  }
+  const bool meta_lane = !is_v && c == 0;  // writes the group's count and positions
+
+  // One wave-wide gather brings every value the step needs: lane l < 39
+  // reads Veil word l of the record; the next lanes read the record's kind,
+  // capacity, patch and block frames, the frame time (two words) and
+  // weight, and the slots' group counts and weight sums (absent optional
+  // inputs read a stand-in address).  Meanwhile the groups' patch chunks in
+  // the frame stream in.
+  constexpr int kGKind = kVeilWords, kGCap = kGKind + 1, kGPatch = kGKind + 2, kGBf = kGKind + 3, kGT = kGKind + 4,
+                kGW = kGKind + 6, kGNg = kGKind + 7, kGWs = kGKind + 9;
+  static_assert(kGWs + 2 <= 64, "one gathered value per lane");
+  const int32_t *rec = reinterpret_cast<const int32_t *>(a.states + h);
+  const int32_t *gp = rec + kVeilWord0 + min(lane, kVeilWords - 1);
+  const int s1 = min(1, MMA - 1);
+  if (lane == kGKind) gp = rec;
+  if (lane == kGCap) gp = rec + offsetof(HeadState, capacity) / 4;
+  if (lane == kGPatch) gp = rec + offsetof(HeadState, patch_size) / 4;
+  if (lane == kGBf) gp = rec + offsetof(HeadState, block_frames) / 4;
+  if (lane == kGT || lane == kGT + 1) gp = reinterpret_cast<const int32_t *>(a.t_vals) + (lane - kGT);
+  if (lane == kGW && a.weights) gp = reinterpret_cast<const int32_t *>(a.weights);
+  if (lane == kGNg || lane == kGNg + 1) gp = ml.accum_num_groups + hs0 + (lane == kGNg ? 0 : s1);
+  if ((lane == kGWs || lane == kGWs + 1) && ml.accum_weight_sum)
+    gp = reinterpret_cast<const int32_t *>(ml.accum_weight_sum + hs0 + (lane == kGWs ? 0 : s1));
+  uint32_t rw = static_cast<uint32_t>(*gp);
+  const uint16_t *src = is_v ? a.src.v : a.src.k;
+  uint4 x[kEvTiles][kTok];
+#pragma unroll
+  for (int j = 0; j < kEvTiles; ++j) {
+    const int gc = min(g[j], grid_ng - 1);
+    const int gbase = (gc / cols) * p * W + (gc % cols) * p;
+#pragma unroll
+    for (int m = 0; m < kTok; ++m)
+      x[j][m] = ld16o(src, h * a.src_hb + c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb);
+  }
+  const int32_t kind = static_cast<int8_t>(lane_word(rw, kGKind) & 0xff);
+  const int32_t cap = lane_word(rw, kGCap), pch = lane_word(rw, kGPatch), bf = lane_word(rw, kGBf);
+  const int64_t t = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(lane_word(rw, kGT + 1))) << 32) |
+                                         static_cast<uint32_t>(lane_word(rw, kGT)));
+  const float fw = a.weights ? __builtin_bit_cast(float, lane_word(rw, kGW)) : 1.0f;
+  const int32_t ng0 = lane_word(rw, kGNg), ng1 = lane_word(rw, kGNg + 1);
+  const float ws0 = ml.accum_weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs)) : 0.0f;
+  const float ws1 = ml.accum_weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs + 1)) : 0.0f;
+  VeilWords vw;
+  vw.count = static_cast<uint32_t>(lane_word(rw, kVlCount));
+  vw.id0 = lane_word(rw, kVlId);
+  vw.id1 = lane_word(rw, kVlId + 1);
+  vw.seen0 = static_cast<uint32_t>(lane_word(rw, kVlSeen));
+  vw.seen1 = static_cast<uint32_t>(lane_word(rw, kVlSeen + 1));
+  vw.done = static_cast<uint32_t>(lane_word(rw, kVlDone));
+
+  const bool veil = kind == SK_MERGE && pch == p;
+  VeilStep s;
+  s.d = skip_desc();
+  if (veil) s = veil_decide(vw, bf, cap, static_cast<int32_t>(t));
+  const FrameDesc d = s.d;
+  const int slot = d.accum_slot, is_new = d.is_new_block, fin = d.finalize_idx;
+  const bool merging = veil && d.kind == PKV_DST_MERGE_ACCUM && slot >= 0 && slot < MMA;
+  const int64_t hs = hs0 + (merging ? slot : 0);
+
+  // Arrival as soon as every wave holds its gather: the head's last
+  // workgroup to arrive knows that no workgroup of the head reads the
+  // record, the slot counts or the weight sums any more (nor, in a block
+  // begun by this call, the slot's group ids), so its write-back waits for
+  // nothing but its own work; the arrival's round trip overlaps the reads
+  // below.
+  __syncthreads();
+  int early = 0;
+  if (tid == 0) early = atomicAdd(a.early + static_cast<int64_t>(h) * kArriveStride, 1);
+
+  // a continued block: its slot's sums, anchor positions and stored group
+  // ids, the ids verified against the grid by a block-wide vote
+  float4 acc[kEvTiles][2];
+  int64_t apos[kEvTiles][3] = {};
+  int ng = grid_ng;
+  float wsum = 0.0f + fw;
+  bool fast = veil;
+  if (merging && !is_new) {
+    int4 ids[kEvIdLoads];
+    const int n4 = FSEQ / 4;
+#pragma unroll
+    for (int k = 0; k < kEvIdLoads; ++k)
+      ids[k] = reinterpret_cast<const int4 *>(ml.accum_group_ids + hs * FSEQ)[min(tid + k * kUpdThreads, n4 - 1)];
+    float *acc_sum = is_v ? ml.accum_sum_v : ml.accum_sum_k;
+#pragma unroll
+    for (int j = 0; j < kEvTiles; ++j) {
+      const float4 *ap = reinterpret_cast<const float4 *>(acc_sum + (hs * MTPA + min(g[j], MTPA - 1)) * D + c);
+      acc[j][0] = ap[0];
+      acc[j][1] = ap[1];
+    }
+    if (meta_lane && fin >= 0) {
+#pragma unroll
+      for (int j = 0; j < kEvTiles; ++j)
+#pragma unroll
+        for (int e = 0; e < 3; ++e) apos[j][e] = ml.accum_pos[(hs * MTPA + min(g[j], MTPA - 1)) * 3 + e];
+    }
+    ng = min(slot ? ng1 : ng0, MTPA);
+    wsum = (slot ? ws1 : ws0) + fw;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < kEvIdLoads; ++k) {
+      const int i = tid + k * kUpdThreads;
+      if (i < n4) {
+        int y = (4 * i) / W, xx = (4 * i) % W;
+        const int32_t v[4] = {ids[k].x, ids[k].y, ids[k].z, ids[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bad |= v[e] != (y / p) * cols + xx / p;
+          if (++xx == W) {
+            xx = 0;
+            ++y;
+          }
+        }
+      }
+    }
+    if (tid == 0) sh.last = early;
+    fast = ng == grid_ng && !__syncthreads_or(bad);
+  } else {
+    if (tid == 0) sh.last = early;
+    __syncthreads();
+  }
+  const bool last = uni(sh.last) == a.n_merge - 1;
+  if (last && tid == 0) atomicExch(a.early + static_cast<int64_t>(h) * kArriveStride, 0);
+  int ticket = 0;
+  if (!fast) {  // update_kernel's merge tiles, with their own arrival (same in every workgroup of the head)
+    upd_merge_wg(a, sh, dyn, h, tile, ticket, kEvTiles);
+    upd_finish(a, sh, h, tile, ticket);
+    return;
+  }
+
+  // the head's last workgroup writes the record's Veil words, the
+  // descriptor and the slot's group count and weight sum first (ahead of
+  // its accumulator stores)
+  if (last) {
+    if (wave == 0) {
+      veil_apply_wave(s, rw);
+      if (lane < kVeilWords) reinterpret_cast<uint32_t *>(a.states + h)[kVeilWord0 + lane] = rw;
+    }
+    if (tid == 0) {
+      store_desc(a.desc, h, 0, h, d);
+      if (merging) {
+        if (is_new) ml.accum_num_groups[hs] = ng;
+        if (ml.accum_weight_sum) ml.accum_weight_sum[hs] = wsum;
+      }
+    }
+  }
+
+  if (merging) {
+    float *acc_sum = is_v ? ml.accum_sum_v : ml.accum_sum_k;
+#pragma unroll
+    for (int j = 0; j < kEvTiles; ++j) {
+      if (!own[j]) continue;
+      const int gj = g[j];
+      float ax[8];
+      if (is_new) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ax[e] = 0.0f;
+      } else {
+        ax[0] = acc[j][0].x; ax[1] = acc[j][0].y; ax[2] = acc[j][0].z; ax[3] = acc[j][0].w;
+        ax[4] = acc[j][1].x; ax[5] = acc[j][1].y; ax[6] = acc[j][1].z; ax[7] = acc[j][1].w;
+      }
+      if (gj < ng) {
+#pragma unroll
+        for (int m = 0; m < kTok; ++m) {
+          const uint32_t xw[4] = {x[j][m].x, x[j][m].y, x[j][m].z, x[j][m].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            ax[2 * e] += fw * bf16_to_f32(static_cast<uint16_t>(xw[e] & 0xffff));
+            ax[2 * e + 1] += fw * bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
+          }
+        }
+      }
+      float4 *ap = reinterpret_cast<float4 *>(acc_sum + (hs * MTPA + gj) * D + c);
+      ap[0] = make_float4(ax[0], ax[1], ax[2], ax[3]);
+      ap[1] = make_float4(ax[4], ax[5], ax[6], ax[7]);
+      const int64_t py = (gj / cols) * p, px = (gj % cols) * p;
+      // a block begun here: the group ids of the group's members, one
+      // member per K-side thread (no workgroup of the head reads them in
+      // this call)
+      if (is_new && !is_v && c < 8 * kTok && gj < ng)
+        ml.accum_group_ids[hs * FSEQ + (gj / cols) * p * W + (gj % cols) * p + (c / 8 / p) * W + (c / 8) % p] = gj;
+      if (is_new && meta_lane) {
+        ml.accum_tokens_per_group[hs * MTPA + gj] =
+            gj < ng ? static_cast<float>(kTok) * static_cast<float>(bf) : 0.0f;
+        if (gj < ng) {
+          int64_t *pp = ml.accum_pos + (hs * MTPA + gj) * 3;
+          pp[0] = t;
+          pp[1] = py;
+          pp[2] = px;
+        }
+      }
+      if (fin >= 0 && fin < a.MMB && gj < ng) {
+        // count * sum(w) for weighted merges, else the reference's count * block_frames
+        const float div = static_cast<float>(kTok) * (a.weights ? wsum : static_cast<float>(bf));
+        const float inv = div > 0.0f ? 1.0f / div : 0.0f;
+        const int64_t hp = static_cast<int64_t>(h) * a.MMB + fin;
+        uint4 ox;
+        ox.x = pack_bf16x2(ax[0] * inv, ax[1] * inv);
+        ox.y = pack_bf16x2(ax[2] * inv, ax[3] * inv);
+        ox.z = pack_bf16x2(ax[4] * inv, ax[5] * inv);
+        ox.w = pack_bf16x2(ax[6] * inv, ax[7] * inv);
+        st16((is_v ? ml.merge_v : ml.merge_k) + (hp * MTPA + gj) * D + c, ox);
+        if (meta_lane) {
+          int64_t *mp = ml.merge_pos + (hp * MTPA + gj) * 3;
+          mp[0] = is_new ? t : apos[j][0];
+          mp[1] = is_new ? py : apos[j][1];
+          mp[2] = is_new ? px : apos[j][2];
+        }
+      }
+    }
+    if (fin >= 0 && fin < a.MMB && tile == 0 && tid == 0) ml.merge_token_count[static_cast<int64_t>(h) * a.MMB + fin] = ng;
+  }
+
 }
 
 // Scratch of pkv_merge_accum_static: the per-(head, frame) merge snapshots
@@ -1595,7 +2019,8 @@ static int merge_scratch_device_ptr(void **out) {
 // hipGetSymbolAddress returns for the current device, looked up once per
 // device.  Calls that overlap on one device (two streams) race on it.
 constexpr int kEvictMaxHeads = 64;
-static __device__ __align__(256) int32_t evict_arrive[kEvictMaxHeads * (kArriveFan + 1) * kArriveStride];
+constexpr int kEvictArriveWords = kEvictMaxHeads * (kArriveFan + 1) * kArriveStride;
+static __device__ __align__(256) int32_t evict_arrive[kEvictArriveWords + kEvictMaxHeads * kArriveStride];
 
 static int evict_arrive_ptr(int32_t **out) {
   static std::mutex mu;
@@ -1795,6 +2220,7 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
   for (int i = 0; i < 8; ++i) dw[i] = reinterpret_cast<int32_t *>(w + i * dbytes);
   u.desc = pkv_state_desc{dw[0], dw[1], dw[2], dw[3], dw[4], dw[5], dw[6], dw[7]};
   u.arrive = reinterpret_cast<int32_t *>(w + 8 * dbytes);
+  u.early = nullptr;
   const int64_t src_bytes = static_cast<int64_t>(F) * FSEQ * a->tok_stride * 2;
   const int64_t max_slots = std::max(std::max(geo->max_sink, geo->max_middle), geo->max_recent);
   if (src_bytes >= (int64_t{1} << 31) || max_slots * FSEQ * D * 2 >= (int64_t{1} << 31))
@@ -1871,6 +2297,7 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
   u.ml = *ml;
   u.desc = *desc;
   u.arrive = arrive;
+  u.early = arrive + kEvictArriveWords;
   u.src_fb = static_cast<uint32_t>(static_cast<int64_t>(H) * FSEQ * D * 2);
   u.src_hb = static_cast<uint32_t>(static_cast<int64_t>(FSEQ) * D * 2);
   u.src_tb = static_cast<uint32_t>(D * 2);
@@ -1882,14 +2309,26 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
   u.MMA = MMA; u.MMB = MMB; u.MTPA = MTPA;
   u.pass_kind = 1;
   u.n_scat = 0;
-  u.n_merge = (MTPA + merge_tile_groups(D) - 1) / merge_tile_groups(D);
   u.n_mh = H;
   u.merge_heads = H >= 64 ? ~uint64_t{0} : (uint64_t{1} << H) - 1;
+  // one frame on a grid of 2 x 2 patches: evict_kernel (which still runs
+  // update_kernel's merge tile for heads its path does not cover)
+  auto al16 = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  const int W = spatial_width;
+  const bool one = F == 1 && MMA <= 2 && W <= FSEQ && FSEQ % W == 0 && W % 2 == 0 && (FSEQ / W) % 2 == 0 &&
+                   FSEQ / 4 <= MTPA && FSEQ <= kEvMaxFseq && D >= 8 * kPreTok && al16(new_k) && al16(new_v) &&
+                   al16(ml->accum_sum_k) && al16(ml->accum_sum_v) && al16(ml->accum_group_ids);
+  const int gpt = one ? evict_tile_groups(D) : merge_tile_groups(D);
+  u.n_merge = (MTPA + gpt - 1) / gpt;
+  const void *kern = one ? reinterpret_cast<const void *>(evict_kernel) : reinterpret_cast<const void *>(update_kernel);
   const size_t smem = static_cast<size_t>(merge_lds_words(FSEQ, MMA)) * sizeof(int32_t);
-  if (smem > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(update_kernel),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          static_cast<int>(smem)) != hipSuccess)
+  if (smem > 65536 &&
+      hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
     return fail(PKV_ERR_HIP, "evict_merge: cannot reserve %zu bytes of LDS", smem);
+  if (one) {
+    hipLaunchKernelGGL(evict_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u);
+    return check_launch("evict_kernel");
+  }
   hipLaunchKernelGGL(update_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u);
   return check_launch("update_kernel");
 }

@@ -24,11 +24,14 @@ pytestmark = pytest.mark.gpu
 D, MMA, MMB, MT = 128, 2, 6, 420
 
 
-def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None):
-    """kinds: per head 'merge' or 'cyclic' (default all 'merge')."""
+def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None, recs=None, tamper=None):
+    """kinds: per head 'merge' or 'cyclic' (default all 'merge'); recs:
+    the records themselves; tamper(ci, acc, dacc): called before call ci
+    (may rewrite host and device accumulators alike)."""
     rng = np.random.default_rng(seed)
     kinds = kinds or ["merge"] * H
-    recs = [O.make_merge(2, int(rng.integers(2, 7))) if k == "merge" else O.make_cyclic(4, 2) for k in kinds]
+    if recs is None:
+        recs = [O.make_merge(2, int(rng.integers(2, 7))) if k == "merge" else O.make_cyclic(4, 2) for k in kinds]
     states_host = O.states_to_bytes(recs)
     states_dev = to_dev(states_host)
     acc = dict(sum_k=np.zeros((H, MMA, MT, D), np.float32), sum_v=np.zeros((H, MMA, MT, D), np.float32),
@@ -42,6 +45,8 @@ def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None):
     tok = np.arange(FSEQ)
     for ci, t_vals in enumerate(calls):
         F = len(t_vals)
+        if tamper is not None:
+            tamper(ci, acc, dacc)
         print(f"evict_merge H={H} FSEQ={FSEQ} W={W} call {ci} t={t_vals} weighted={weighted}", flush=True)
         nk = O.f32_to_bf16(rng.standard_normal((F, H, FSEQ, D)).astype(np.float32))
         nv = O.f32_to_bf16(rng.standard_normal((F, H, FSEQ, D)).astype(np.float32))
@@ -89,3 +94,40 @@ def test_evict_irregular_grid_and_mixed_heads():
     # only)
     calls = [[5 * b + f for f in range(5)] for b in range(5)]
     _evict_run(H=3, FSEQ=7 * 9 + 3, W=7, calls=calls, seed=2, weighted=True, kinds=["merge", "cyclic", "merge"])
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+def test_evict_one_frame_out_of_order_and_repeated(weighted):
+    # one frame per call in random order with repeats: blocks begun while both
+    # accumulator slots are busy (slot 0 evicted), repeated frames (skipped),
+    # completed-FIFO shifts at capacities 2 and 3
+    rng = np.random.default_rng(31 + weighted)
+    calls = [[int(t)] for t in rng.integers(0, 28, 48)]
+    recs = [O.make_merge(2, 2), O.make_merge(2, 3), O.make_merge(2, 6)]
+    _evict_run(H=3, FSEQ=1560, W=52, calls=calls, seed=5, weighted=weighted, recs=recs)
+
+
+def test_evict_one_frame_mixed_kinds_and_patch_sizes():
+    # on the regular grid: a Wave head, a patch-1 Veil head (one-frame blocks)
+    # and an Anchor head beside patch-2 Veil heads
+    recs = [O.make_merge(2, 4), O.make_cyclic(4, 2), O.make_merge(1, 3), O.make_stride(2, 3), O.make_merge(2, 2)]
+    _evict_run(H=5, FSEQ=1560, W=52, calls=[[e] for e in range(20)], seed=6, weighted=True, recs=recs)
+
+
+@pytest.mark.parametrize("how", ["permuted", "swapped_pair"])
+def test_evict_one_frame_continues_block_by_its_stored_group_ids(how):
+    # a block's stored group ids rewritten between its frames (host and
+    # device alike): its later frames follow the stored ids, not the grid
+    def tamper(ci, acc, dacc):
+        if ci != 2:
+            return
+        gid = acc["gid"]
+        rng = np.random.default_rng(9)
+        for h in range(gid.shape[0]):
+            for s in range(gid.shape[1]):
+                if how == "permuted":
+                    gid[h, s] = gid[h, s][rng.permutation(gid.shape[2])]
+                else:  # tokens 0 and 60 (groups 0 and 4 of the grid) trade ids
+                    gid[h, s, 0], gid[h, s, 60] = gid[h, s, 60].copy(), gid[h, s, 0].copy()
+        dacc["gid"].copy_(to_dev(gid))
+    _evict_run(H=2, FSEQ=1560, W=52, calls=[[e] for e in range(10)], seed=7, weighted=True, tamper=tamper)
