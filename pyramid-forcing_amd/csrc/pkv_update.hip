@@ -828,6 +828,13 @@ __device__ inline uint4 ld16o(const void *base, uint32_t off) {
 __device__ inline void st16o(void *base, uint32_t off, uint4 v) {
   *reinterpret_cast<uint4 *>(static_cast<char *>(base) + off) = v;
 }
+// the same load with the non-temporal (streaming) cache policy, for data
+// read once
+__device__ inline uint4 ld16o_nt(const void *base, uint32_t off) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(static_cast<const char *>(base) + off));
+  return make_uint4(q.x, q.y, q.z, q.w);
+}
 static_assert(kStateWords <= kUpdThreads, "one state word per thread");
 
 // list sources of a merge frame's groups
@@ -1578,16 +1585,16 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
   upd_finish(a, sh, h, merge_tile ? tile : (is_merge_head(a, h) ? a.n_merge : 0) + tile, ticket);
 }
 
-// ---- Veil eviction of one frame per call (pkv_evict_merge) ----------------
+// ---- Veil step in registers ------------------------------------------------
 //
 // A Veil step (anchor_store_update.cu:122-231) changes only the record's
 // last 39 words: the completed FIFO, the active blocks' ids, seen flags and
 // frame counts.  The step splits into a decision -- scalar arithmetic on
 // six of those words, the block frames and the capacity -- and its
 // application to the words, one word per lane of a wave (the FIFO shift
-// reads the next lane's word).  That replaces the state machine on one
-// thread over the LDS record, whose chain of dependent LDS accesses was the
-// longest step of an eviction.
+// reads the next lane's word).  The eviction kernel uses it in place of the
+// state machine on one thread over the LDS record, whose chain of dependent
+// LDS accesses was the longest step of an eviction.
 constexpr int kVeilWord0 = static_cast<int>(offsetof(HeadState, merge_completed_slot) / 4);
 constexpr int kVeilWords = kStateWords - kVeilWord0;
 constexpr int kVlCount = static_cast<int>(offsetof(HeadState, merge_completed_count) / 4) - kVeilWord0;
@@ -1725,6 +1732,8 @@ __device__ inline void veil_apply_wave(const VeilStep &s, uint32_t &w) {
   w = veil_apply(s, w, next, lane);
 }
 
+// ---- Veil eviction of one frame per call (pkv_evict_merge) ----------------
+//
 // Eviction workgroups cover kEvTiles of update_kernel's merge tiles (each
 // thread kEvTiles groups, same roles), so that the per-workgroup reads (the
 // record, the stored group ids) and the arrivals are fewer.
@@ -1798,7 +1807,7 @@ __global__ void __launch_bounds__(kUpdThreads) evict_kernel(UpdArgs a) {
     const int gbase = (gc / cols) * p * W + (gc % cols) * p;
 #pragma unroll
     for (int m = 0; m < kTok; ++m)
-      x[j][m] = ld16o(src, h * a.src_hb + c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb);
+      x[j][m] = ld16o_nt(src, h * a.src_hb + c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb);
   }
   const int32_t kind = static_cast<int8_t>(lane_word(rw, kGKind) & 0xff);
   const int32_t cap = lane_word(rw, kGCap), pch = lane_word(rw, kGPatch), bf = lane_word(rw, kGBf);
