@@ -628,6 +628,10 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
     if (row_q < Lq) v = ldg16(qp + static_cast<int64_t>(row_q) * p.q_tok + 16 * s + 8 * hf);
     qr[s] = as_bf16x8(v);
   }
+  // Q is in registers before the first tile copy is issued: the compiler,
+  // which cannot see the copies, then has no load of its own pending in the
+  // key loop, where a wait for one would also wait for every copy in flight
+  wait_vm<0>();
   f32x16 o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db)
