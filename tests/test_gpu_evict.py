@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 D, MMA, MMB, MT = 128, 2, 6, 420
 
 
-def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None, recs=None, tamper=None):
+def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None, recs=None, tamper=None, D=D):
     """kinds: per head 'merge' or 'cyclic' (default all 'merge'); recs:
     the records themselves; tamper(ci, acc, dacc): called before call ci
     (may rewrite host and device accumulators alike)."""
@@ -131,3 +131,9 @@ def test_evict_one_frame_continues_block_by_its_stored_group_ids(how):
                     gid[h, s, 0], gid[h, s, 60] = gid[h, s, 60].copy(), gid[h, s, 0].copy()
         dacc["gid"].copy_(to_dev(gid))
     _evict_run(H=2, FSEQ=1560, W=52, calls=[[e] for e in range(10)], seed=7, weighted=True, tamper=tamper)
+
+
+def test_evict_one_frame_head_dim_64():
+    # head_dim 64: 8 chunks per group row, twice the groups per workgroup
+    calls = [[int(t)] for t in np.random.default_rng(12).integers(0, 20, 24)]
+    _evict_run(H=3, FSEQ=1560, W=52, calls=calls, seed=12, weighted=True, D=64)
