@@ -250,7 +250,9 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
   const int32_t *mts = staged ? s_mtc : mtc;
   const int wave = tid >> 6, n_waves = blockDim.x >> 6, lane = tid & 63;
   const int n_cand = p.max_sink + p.max_recent + kMaxTKeyed + kMaxMergeBlocks;
-  if (n_cand <= 64 && p.S <= 64 && pairs <= 64 && pairs <= n_waves * kPlanRegRounds) {
+  // (the one-pass form reads the staged copies by their LDS arrays, so that
+  // the compiler issues LDS reads rather than generic ones)
+  if (staged && n_cand <= 64 && p.S <= 64 && pairs <= 64 && pairs <= n_waves * kPlanRegRounds) {
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     Cand cd[kPlanRegRounds];
     int pos[kPlanRegRounds], excl[kPlanRegRounds], nv[kPlanRegRounds];
@@ -262,8 +264,8 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(PlanParams p, const 
       pos[r] = excl[r] = nv[r] = 0;
       if (q < pairs) {  // uniform over the wave
         const int c = q / p.H, h = q % p.H;
-        const PairCtx x = pair_ctx(p, st[h], vcs + h * 3, c);
-        cd[r] = eval_cand(p, st[h], mts + h * p.MMB, x, h, lane);
+        const PairCtx x = pair_ctx(p, s_states[h], s_vc + h * 3, c);
+        cd[r] = eval_cand(p, s_states[h], s_mtc + h * p.MMB, x, h, lane);
         const uint64_t mask = __ballot(cd[r].valid);
         pos[r] = __popcll(mask & below);
         emit[r] = cd[r].valid && pos[r] < p.S;
