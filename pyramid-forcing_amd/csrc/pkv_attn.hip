@@ -788,19 +788,13 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
       constexpr int TT = decltype(tt_c)::value;
       f32x16 &scur = (TT & 1) ? sb : sa;
       f32x16 &snext = (TT & 1) ? sa : sb;
-      // I0: S(t+1) MFMAs with P(t)'s exponentials in their shadow: each
-      // MFMA of the dependent chain is followed by two exponentials and the
-      // arithmetic around them
+      // I0: S(t+1) MFMAs with P(t)'s exponentials in their shadow (the
+      // compiler's own interleaving: pinning one MFMA between every two
+      // exponentials with scheduling-group barriers ran 0.8% slower)
       gemm0(snext);
       const float ps = probs(scur, m, pb);
       l += ps;
       ovf |= !(ps < exp2f(kHeadroom));
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // transcendental
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // other VALU
-      }
       pp_barrier();
       // I1: V(t) to registers, copy of K(t+4); K(t+2) complete after the wait
       load_v(vslot(ic<TT>()));
