@@ -437,6 +437,7 @@ def bench_merge(steps: int, warmup: int, seed: int = 0):
                mpos=torch.zeros(H, MMB, MT, 3, dtype=torch.int64, device=dev),
                mtc=torch.zeros(H, MMB, dtype=torch.int32, device=dev))
     desc = [torch.full((H,), -1, dtype=torch.int32, device=dev) for _ in range(8)]
+    ws = torch.zeros(ops.mega_evict_merge_workspace_size(H), dtype=torch.uint8, device=dev)
     init = {n_: t.clone() for n_, t in acc.items()}
 
     def reset():
@@ -448,7 +449,7 @@ def bench_merge(steps: int, warmup: int, seed: int = 0):
         for e in range(EVICTIONS):
             ops.mega_evict_merge(states, tv[e], nk[e], nv[e], 52, w[e:e + 1], *desc, acc["sum_k"], acc["sum_v"],
                                  acc["pos"], acc["gid"], acc["tpg"], acc["ng"], acc["wsum"], acc["mk"], acc["mv"],
-                                 acc["mpos"], acc["mtc"])
+                                 acc["mpos"], acc["mtc"], ws)
 
     reset()
     step()

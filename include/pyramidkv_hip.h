@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PKV_ABI_VERSION 2
+#define PKV_ABI_VERSION 3
 
 typedef void *pkv_stream_t; /* hipStream_t; NULL selects the null stream */
 
@@ -364,13 +364,16 @@ typedef struct pkv_update_args {
  * in the reference, which evicts through mega_state_update
  * (anchor_store_update.cu:257-269) and mega_merge_accum
  * (mega_merge_accum.cu:52-340); it is for callers that evict frames
- * outside MegaCache.update.  Arrival counters live in a static device
- * array: calls that overlap on one device race. */
+ * outside MegaCache.update.  workspace: pkv_evict_merge_workspace_size
+ * bytes of arrival counters, zero-filled before first use; every call
+ * leaves them zero.  Calls that share a workspace must not overlap. */
 int pkv_evict_merge(uint8_t *states, int32_t num_heads, int32_t frames, int32_t frame_seqlen, int32_t head_dim,
                     int32_t max_merge_active, int32_t max_merge_blocks, int32_t max_merge_tokens,
                     const int64_t *t_vals, const uint16_t *new_k, const uint16_t *new_v, int32_t spatial_width,
                     const float *frame_weights, const pkv_state_desc *desc, const pkv_merge_layer *ml,
-                    pkv_stream_t stream);
+                    void *workspace, pkv_stream_t stream);
+/* Workspace bytes pkv_evict_merge needs for num_heads heads. */
+int64_t pkv_evict_merge_workspace_size(int32_t num_heads);
 
 /* MegaCache.update of one layer (_mega_cache.py:136-414) in one launch:
  * sink / recent routing of the F new frames with the recent FIFO shift, the

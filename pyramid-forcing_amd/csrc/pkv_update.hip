@@ -2022,32 +2022,11 @@ static int merge_scratch_device_ptr(void **out) {
   return PKV_OK;
 }
 
-// Arrival counters of pkv_evict_merge (the caller passes no workspace): a
-// file-scope device array, zero at load and left zero by every call, each
-// device holding its own copy; host code uses only the address that
-// hipGetSymbolAddress returns for the current device, looked up once per
-// device.  Calls that overlap on one device (two streams) race on it.
-constexpr int kEvictMaxHeads = 64;
-constexpr int kEvictArriveWords = kEvictMaxHeads * (kArriveFan + 1) * kArriveStride;
-static __device__ __align__(256) int32_t evict_arrive[kEvictArriveWords + kEvictMaxHeads * kArriveStride];
-
-static int evict_arrive_ptr(int32_t **out) {
-  static std::mutex mu;
-  static int32_t *dev_ptr[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-    return fail(PKV_ERR_HIP, "evict_merge: no current device");
-  std::lock_guard<std::mutex> lock(mu);
-  if (!dev_ptr[dev]) {
-    void *p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(evict_arrive));
-    if (e != hipSuccess)
-      return fail(PKV_ERR_HIP, "evict_merge: hipGetSymbolAddress of the arrival counters failed: %s",
-                  hipGetErrorString(e));
-    dev_ptr[dev] = static_cast<int32_t *>(p);
-  }
-  *out = dev_ptr[dev];
-  return PKV_OK;
+// Workspace of pkv_evict_merge: per head the two-level arrival counters of
+// update_kernel's merge tiles (kArriveFan + 1 lines) and the eviction
+// kernel's arrival counter (one line), each a 128-byte line.
+static int64_t evict_ws_bytes(int H) {
+  return static_cast<int64_t>(H) * (kArriveFan + 2) * kArriveStride * 4;
 }
 
 static PoolPtrs pool_ptrs(const pkv_geometry *g, const pkv_pools *p) {
@@ -2274,10 +2253,10 @@ int pkv_cache_update(const pkv_geometry *geo, const pkv_pools *pools, const pkv_
 int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t D, int32_t MMA, int32_t MMB,
                     int32_t MTPA, const int64_t *t_vals, const uint16_t *new_k, const uint16_t *new_v,
                     int32_t spatial_width, const float *frame_weights, const pkv_state_desc *desc,
-                    const pkv_merge_layer *ml, pkv_stream_t stream) {
+                    const pkv_merge_layer *ml, void *workspace, pkv_stream_t stream) {
   if (H == 0 || F == 0) return PKV_OK;
-  if (!states || !t_vals || !new_k || !new_v || !desc || !ml || H < 0 || F < 0 || FSEQ <= 0 || D <= 0 || MMA <= 0 ||
-      MMB <= 0 || MTPA <= 0)
+  if (!states || !t_vals || !new_k || !new_v || !desc || !ml || !workspace || H < 0 || F < 0 || FSEQ <= 0 ||
+      D <= 0 || MMA <= 0 || MMB <= 0 || MTPA <= 0)
     return fail(PKV_ERR_INVALID, "evict_merge: bad arguments");
   if (!desc->dst_kind || !desc->dst_slot || !desc->src_frame || !desc->src_head || !desc->merge_accum_slot ||
       !desc->merge_local_idx || !desc->merge_finalize_completed_idx || !desc->merge_is_new_block)
@@ -2285,7 +2264,6 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
   if (frame_weights && !ml->accum_weight_sum)
     return fail(PKV_ERR_INVALID, "evict_merge: weighted merge needs accum_weight_sum");
   if (spatial_width <= 0) return fail(PKV_ERR_INVALID, "evict_merge: spatial_width must be > 0");
-  if (H > kEvictMaxHeads) return fail(PKV_ERR_UNSUPPORTED, "evict_merge: %d heads exceed %d", H, kEvictMaxHeads);
   if (F > kUpdMaxFrames) return fail(PKV_ERR_UNSUPPORTED, "evict_merge: %d frames exceed %d", F, kUpdMaxFrames);
   if (D % 8 != 0 || D / 8 > 64)
     return fail(PKV_ERR_UNSUPPORTED, "evict_merge: head_dim %d must be a multiple of 8, at most 512", D);
@@ -2297,16 +2275,14 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
     return fail(PKV_ERR_UNSUPPORTED, "evict_merge: %d active merge blocks exceed %d", MMA, kMaxMergeSlots);
   if (static_cast<int64_t>(F) * H * FSEQ * D * 2 >= (int64_t{1} << 31))
     return fail(PKV_ERR_UNSUPPORTED, "evict_merge: the new frames exceed 2 GiB");
-  int32_t *arrive = nullptr;
-  int rc = evict_arrive_ptr(&arrive);
-  if (rc) return rc;
+  int32_t *arrive = static_cast<int32_t *>(workspace);
   UpdArgs u{};
   u.states = reinterpret_cast<HeadState *>(states);
   u.src = FrameSrc{new_k, new_v, static_cast<int64_t>(H) * FSEQ * D, static_cast<int64_t>(FSEQ) * D, D};
   u.ml = *ml;
   u.desc = *desc;
   u.arrive = arrive;
-  u.early = arrive + kEvictArriveWords;
+  u.early = arrive + static_cast<int64_t>(H) * (kArriveFan + 1) * kArriveStride;
   u.src_fb = static_cast<uint32_t>(static_cast<int64_t>(H) * FSEQ * D * 2);
   u.src_hb = static_cast<uint32_t>(static_cast<int64_t>(FSEQ) * D * 2);
   u.src_tb = static_cast<uint32_t>(D * 2);
@@ -2340,6 +2316,10 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
   }
   hipLaunchKernelGGL(update_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u);
   return check_launch("update_kernel");
+}
+
+int64_t pkv_evict_merge_workspace_size(int32_t num_heads) {
+  return num_heads > 0 ? evict_ws_bytes(num_heads) : 0;
 }
 
 }  // extern "C"

@@ -530,7 +530,7 @@ static void mega_evict_merge(Tensor states, Tensor new_t_vals, Tensor new_k, Ten
                              c10::optional<Tensor> frame_weights, Tensor d0, Tensor d1, Tensor d2, Tensor d3,
                              Tensor d4, Tensor d5, Tensor d6, Tensor d7, Tensor acc_k, Tensor acc_v, Tensor acc_pos,
                              Tensor acc_gid, Tensor acc_tpg, Tensor acc_ng, Tensor acc_wsum, Tensor mk, Tensor mv,
-                             Tensor mpos, Tensor mtc) {
+                             Tensor mpos, Tensor mtc, Tensor workspace) {
   TORCH_CHECK(new_k.is_cuda() && new_k.dtype() == at::kBFloat16 && new_v.sizes() == new_k.sizes() &&
                   new_v.dtype() == at::kBFloat16,
               "mega_evict_merge: new_k/new_v must be CUDA bf16 of equal shape");
@@ -554,6 +554,10 @@ static void mega_evict_merge(Tensor states, Tensor new_t_vals, Tensor new_k, Ten
   TORCH_CHECK(acc_k.dim() == 4 && acc_k.size(3) == D && acc_gid.dim() == 3 && acc_gid.size(2) == FSEQ,
               "mega_evict_merge: accumulators must be [H, MMA, MTPA, D] with group ids [H, MMA, FSEQ]");
   const int64_t MMA = acc_k.size(1), MMB = mk.size(1), MTPA = acc_k.size(2);
+  TORCH_CHECK(workspace.is_cuda() && workspace.is_contiguous() &&
+                  workspace.numel() * workspace.element_size() >= pkv_evict_merge_workspace_size(static_cast<int32_t>(H)),
+              "mega_evict_merge: workspace must be a contiguous CUDA tensor of at least "
+              "mega_evict_merge_workspace_size(num_heads) bytes, zero-filled before first use");
   if (H == 0 || F == 0) return;
   auto nk = new_k.contiguous(), nv = new_v.contiguous();
   auto tv = new_t_vals.contiguous();
@@ -574,8 +578,14 @@ static void mega_evict_merge(Tensor states, Tensor new_t_vals, Tensor new_k, Ten
                             static_cast<int32_t>(MMB), static_cast<int32_t>(MTPA), tv.data_ptr<int64_t>(),
                             reinterpret_cast<const uint16_t *>(nk.data_ptr()),
                             reinterpret_cast<const uint16_t *>(nv.data_ptr()), static_cast<int32_t>(spatial_width),
-                            frame_weights ? w.data_ptr<float>() : nullptr, &desc, &ml, stream_for(nk)),
+                            frame_weights ? w.data_ptr<float>() : nullptr, &desc, &ml, workspace.data_ptr(),
+                            stream_for(nk)),
             "mega_evict_merge");
+}
+
+// Bytes of the arrival-counter workspace mega_evict_merge needs.
+static int64_t mega_evict_merge_workspace_size(int64_t num_heads) {
+  return pkv_evict_merge_workspace_size(static_cast<int32_t>(num_heads));
 }
 
 // ---------------------------------------------------------------------------
@@ -1144,7 +1154,8 @@ TORCH_LIBRARY(adahead, m) {
         "Tensor(k!) accum_sum_v, Tensor(l!) accum_pos, Tensor(m!) accum_group_ids, "
         "Tensor(n!) accum_tokens_per_group, Tensor(o!) accum_num_groups, Tensor(p!) accum_weight_sum, "
         "Tensor(q!) merge_k_pool, Tensor(r!) merge_v_pool, Tensor(s!) merge_pos_pool, "
-        "Tensor(t!) merge_token_count) -> ()");
+        "Tensor(t!) merge_token_count, Tensor(u!) workspace) -> ()");
+  m.def("mega_evict_merge_workspace_size(int num_heads) -> int");
   m.def("mega_merge_accum_weighted(Tensor states, Tensor new_k, Tensor new_v, Tensor new_pos, Tensor desc_dst_kind, "
         "Tensor desc_merge_accum_slot, Tensor desc_merge_finalize_completed_idx, Tensor desc_merge_is_new_block, "
         "Tensor frame_weights, Tensor(a!) accum_sum_k, Tensor(b!) accum_sum_v, Tensor(c!) accum_pos, "
@@ -1206,6 +1217,7 @@ TORCH_LIBRARY_IMPL(adahead, CUDA, m) {
 // dispatch the same implementation whatever the tensor backend.
 TORCH_LIBRARY_IMPL(adahead, CompositeExplicitAutograd, m) {
   m.impl("mega_state_perhead_size", adahead::mega_state_perhead_size);
+  m.impl("mega_evict_merge_workspace_size", adahead::mega_evict_merge_workspace_size);
   m.impl("mega_plan", adahead::mega_plan);
   m.impl("mega_plan_multi", adahead::mega_plan_multi);
   m.impl("update_descriptors", adahead::update_descriptors);

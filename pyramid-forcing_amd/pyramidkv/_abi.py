@@ -101,7 +101,9 @@ def lib():
         L.pkv_merge_accum_static.argtypes = [_c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32] + \
             [_c_p] * 10
         L.pkv_evict_merge.argtypes = [_c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p,
-                                      _c_i32, _c_p, _c_p, _c_p, _c_p]
+                                      _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p]
+        L.pkv_evict_merge_workspace_size.restype = _c_i64
+        L.pkv_evict_merge_workspace_size.argtypes = [_c_i32]
         _lib = L
     return _lib
 

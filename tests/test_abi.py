@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_queries():
     lib = A.lib()
-    assert lib.pkv_abi_version() == 2
+    assert lib.pkv_abi_version() == 3
     assert lib.pkv_perhead_state_size() == 600
     g = A.make_geometry(30, 12, 128, 1560, 3, 24, 4, 8 * 12 * 37 * 1560)
     assert lib.pkv_cache_update_workspace_size(ctypes.byref(g), 3) > 8 * 36 * 4

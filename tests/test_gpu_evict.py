@@ -42,6 +42,7 @@ def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None, recs=None, tamper=
                mtc=np.zeros((H, MMB), np.int32))
     dacc = {k: to_dev(v) for k, v in acc.items()}
     ops = _ops.ops()
+    ws = torch.zeros(ops.mega_evict_merge_workspace_size(H), dtype=torch.uint8, device=DEV)
     tok = np.arange(FSEQ)
     for ci, t_vals in enumerate(calls):
         F = len(t_vals)
@@ -64,7 +65,7 @@ def _evict_run(H, FSEQ, W, calls, seed, weighted, kinds=None, recs=None, tamper=
                              to_dev(nk).view(F, H, FSEQ, D), to_dev(nv).view(F, H, FSEQ, D), W,
                              to_dev(w) if w is not None else None, *dd, dacc["sum_k"], dacc["sum_v"], dacc["pos"],
                              dacc["gid"], dacc["tpg"], dacc["ng"], dacc["wsum"], dacc["mk"], dacc["mv"],
-                             dacc["mpos"], dacc["mtc"])
+                             dacc["mpos"], dacc["mtc"], ws)
         torch.cuda.synchronize()
         assert np.array_equal(to_np(states_dev), states_host), f"call {ci}: state records differ"
         for i in range(8):

@@ -202,6 +202,7 @@ def test_config4_weighted_evictions():
     dacc1 = {n: to_dev(a) for n, a in acc.items()}
     desc1 = [torch.full((H,), -1, dtype=torch.int32, device=DEV) for _ in range(8)]
     tok = np.arange(FSEQ)
+    ws = torch.zeros(ops.mega_evict_merge_workspace_size(H), dtype=torch.uint8, device=DEV)
     for e in range(E):
         k = O.f32_to_bf16(rng.standard_normal((1, H, FSEQ, D)).astype(np.float32))
         v = O.f32_to_bf16(rng.standard_normal((1, H, FSEQ, D)).astype(np.float32))
@@ -220,7 +221,7 @@ def test_config4_weighted_evictions():
         ops.mega_evict_merge(sd1, torch.tensor([e + 1], dtype=torch.int64, device=DEV), to_dev(k).view(torch.bfloat16),
                              to_dev(v).view(torch.bfloat16), 52, to_dev(w), *desc1, dacc1["sum_k"], dacc1["sum_v"],
                              dacc1["pos"], dacc1["gid"], dacc1["tpg"], dacc1["ng"], dacc1["wsum"], dacc1["mk"],
-                             dacc1["mv"], dacc1["mpos"], dacc1["mtc"])
+                             dacc1["mv"], dacc1["mpos"], dacc1["mtc"], ws)
     torch.cuda.synchronize()
     assert np.array_equal(to_np(sd), states)
     assert np.array_equal(to_np(sd1), states), "mega_evict_merge: state records differ"

@@ -126,7 +126,7 @@ def test_map_dynamic_pos_time_modes():
 
 
 REQUIRED_OPS = ["pyramidkv_pack", "pyramidkv_update", "mega_state_update", "mega_plan", "mega_plan_multi",
-                "mega_state_perhead_size", "mega_merge_accum", "mega_merge_accum_weighted", "mega_evict_merge",
+                "mega_state_perhead_size", "mega_merge_accum", "mega_merge_accum_weighted", "mega_evict_merge", "mega_evict_merge_workspace_size",
                 "ragged_attention",
                 "rope_apply", "cache_update", "update_descriptors", "mega_attend_kv", "dit_layer_norm", "dit_rms_norm",
                 "dit_residual_", "dit_gelu_tanh", "dit_residual_layer_norm_"]
