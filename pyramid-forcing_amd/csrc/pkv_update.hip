@@ -828,12 +828,19 @@ __device__ inline uint4 ld16o(const void *base, uint32_t off) {
 __device__ inline void st16o(void *base, uint32_t off, uint4 v) {
   *reinterpret_cast<uint4 *>(static_cast<char *>(base) + off) = v;
 }
-// the same load with the non-temporal (streaming) cache policy, for data
-// read once
-__device__ inline uint4 ld16o_nt(const void *base, uint32_t off) {
+// 16-byte raw buffer load at byte offset off with the non-temporal
+// (streaming) cache policy, for data read once: the address is a 32-bit
+// offset from a buffer resource (word 3: 32-bit format, no swizzle; reads
+// past num_records return zero)
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kCpolNt = 2;  // buffer instruction cache policy: non-temporal
+__device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, int num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, num_records, kRsrcWord3);
+}
+__device__ inline uint4 bld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(static_cast<const char *>(base) + off));
-  return make_uint4(q.x, q.y, q.z, q.w);
+  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, kCpolNt);
+  return make_uint4(q[0], q[1], q[2], q[3]);
 }
 static_assert(kStateWords <= kUpdThreads, "one state word per thread");
 
@@ -1754,16 +1761,48 @@ __host__ __device__ inline int evict_tile_groups(int D) { return kEvTiles * merg
 // W = spatial width tiles into 2 x 2 patches with at most MTPA of them, with
 // at most 2 accumulator slots, FSEQ <= kEvMaxFseq, head_dim >= 32 and
 // 16-byte aligned frames, sums and group ids (pkv_evict_merge checks).
-__global__ void __launch_bounds__(kUpdThreads) evict_kernel(UpdArgs a) {
+// The values the first reads need come as leading scalar arguments, which
+// the build preloads into scalar registers (-amdgpu-kernarg-preload-count),
+// so that the gather does not wait for a kernel-argument load; they repeat
+// fields of a.
+__global__ void __launch_bounds__(kUpdThreads)
+    evict_kernel(const HeadState *states, const int64_t *t_vals, const float *weights, const int32_t *num_groups,
+                 const float *weight_sum, int32_t n_merge, int32_t mma, UpdArgs a) {
   extern __shared__ __attribute__((aligned(16))) int32_t dyn[];
   __shared__ __attribute__((aligned(16))) UpdShared sh;
   __shared__ uint32_t vote[kUpdThreads / 64];
   constexpr int p = kPrePatch, kTok = kPreTok;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.x / a.n_merge, tile = blockIdx.x % a.n_merge;
-  const int FSEQ = a.FSEQ, D = a.D, MTPA = a.MTPA, MMA = a.MMA, W = a.width;
+  const int h = blockIdx.x / n_merge, tile = blockIdx.x % n_merge;
+  const int64_t hs0 = static_cast<int64_t>(h) * mma;
+
+  // One wave-wide gather brings every value the step needs, issued first
+  // (its addresses need only the preloaded arguments): lane l < 39 reads
+  // Veil word l of the record; the next lanes read the record's kind,
+  // capacity, patch and block frames, the frame time (two words) and
+  // weight, and the slots' group counts and weight sums (absent optional
+  // inputs read a stand-in address).  Meanwhile the groups' patch chunks in
+  // the frame stream in.
+  constexpr int kGKind = kVeilWords, kGCap = kGKind + 1, kGPatch = kGKind + 2, kGBf = kGKind + 3, kGT = kGKind + 4,
+                kGW = kGKind + 6, kGNg = kGKind + 7, kGWs = kGKind + 9;
+  static_assert(kGWs + 2 <= 64, "one gathered value per lane");
+  const int32_t *rec = reinterpret_cast<const int32_t *>(states + h);
+  const int32_t *gp = rec + kVeilWord0 + min(lane, kVeilWords - 1);
+  const int s1 = min(1, mma - 1);
+  if (lane == kGKind) gp = rec;
+  if (lane == kGCap) gp = rec + offsetof(HeadState, capacity) / 4;
+  if (lane == kGPatch) gp = rec + offsetof(HeadState, patch_size) / 4;
+  if (lane == kGBf) gp = rec + offsetof(HeadState, block_frames) / 4;
+  if (lane == kGT || lane == kGT + 1) gp = reinterpret_cast<const int32_t *>(t_vals) + (lane - kGT);
+  if (lane == kGW && weights) gp = reinterpret_cast<const int32_t *>(weights);
+  if (lane == kGNg || lane == kGNg + 1) gp = num_groups + hs0 + (lane == kGNg ? 0 : s1);
+  if ((lane == kGWs || lane == kGWs + 1) && weight_sum)
+    gp = reinterpret_cast<const int32_t *>(weight_sum + hs0 + (lane == kGWs ? 0 : s1));
+  uint32_t rw = static_cast<uint32_t>(*gp);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int FSEQ = a.FSEQ, D = a.D, MTPA = a.MTPA, MMA = mma, W = a.width;
   const int cols = W / p, grid_ng = FSEQ / (p * p);
-  const int64_t hs0 = static_cast<int64_t>(h) * MMA;
   const pkv_merge_layer &ml = a.ml;
   const MergeLane ln0(a, tile * kEvTiles);
   const int c = ln0.c, is_v = ln0.is_v;
@@ -1776,47 +1815,28 @@ __global__ void __launch_bounds__(kUpdThreads) evict_kernel(UpdArgs a) {
     own[j] = ln.own;
   }
   const bool meta_lane = !is_v && c == 0;  // writes the group's count and positions
-
-  // One wave-wide gather brings every value the step needs: lane l < 39
-  // reads Veil word l of the record; the next lanes read the record's kind,
-  // capacity, patch and block frames, the frame time (two words) and
-  // weight, and the slots' group counts and weight sums (absent optional
-  // inputs read a stand-in address).  Meanwhile the groups' patch chunks in
-  // the frame stream in.
-  constexpr int kGKind = kVeilWords, kGCap = kGKind + 1, kGPatch = kGKind + 2, kGBf = kGKind + 3, kGT = kGKind + 4,
-                kGW = kGKind + 6, kGNg = kGKind + 7, kGWs = kGKind + 9;
-  static_assert(kGWs + 2 <= 64, "one gathered value per lane");
-  const int32_t *rec = reinterpret_cast<const int32_t *>(a.states + h);
-  const int32_t *gp = rec + kVeilWord0 + min(lane, kVeilWords - 1);
-  const int s1 = min(1, MMA - 1);
-  if (lane == kGKind) gp = rec;
-  if (lane == kGCap) gp = rec + offsetof(HeadState, capacity) / 4;
-  if (lane == kGPatch) gp = rec + offsetof(HeadState, patch_size) / 4;
-  if (lane == kGBf) gp = rec + offsetof(HeadState, block_frames) / 4;
-  if (lane == kGT || lane == kGT + 1) gp = reinterpret_cast<const int32_t *>(a.t_vals) + (lane - kGT);
-  if (lane == kGW && a.weights) gp = reinterpret_cast<const int32_t *>(a.weights);
-  if (lane == kGNg || lane == kGNg + 1) gp = ml.accum_num_groups + hs0 + (lane == kGNg ? 0 : s1);
-  if ((lane == kGWs || lane == kGWs + 1) && ml.accum_weight_sum)
-    gp = reinterpret_cast<const int32_t *>(ml.accum_weight_sum + hs0 + (lane == kGWs ? 0 : s1));
-  uint32_t rw = static_cast<uint32_t>(*gp);
-  const uint16_t *src = is_v ? a.src.v : a.src.k;
+  // (loaded through a buffer resource of the head's frame: 32-bit offsets)
+  const __amdgpu_buffer_rsrc_t srsrc = buf_rsrc(
+      reinterpret_cast<const char *>(is_v ? a.src.v : a.src.k) + static_cast<uint64_t>(h) * a.src_hb,
+      static_cast<int>((FSEQ - 1) * a.src_tb + D * 2));
   uint4 x[kEvTiles][kTok];
 #pragma unroll
   for (int j = 0; j < kEvTiles; ++j) {
     const int gc = min(g[j], grid_ng - 1);
     const int gbase = (gc / cols) * p * W + (gc % cols) * p;
 #pragma unroll
-    for (int m = 0; m < kTok; ++m)
-      x[j][m] = ld16o_nt(src, h * a.src_hb + c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb);
+    for (int m = 0; m < kTok; ++m) x[j][m] = bld16_nt(srsrc, c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb);
   }
+  // the chunk loads stay issued ahead of the first use of the gather
+  __builtin_amdgcn_sched_barrier(0);
   const int32_t kind = static_cast<int8_t>(lane_word(rw, kGKind) & 0xff);
   const int32_t cap = lane_word(rw, kGCap), pch = lane_word(rw, kGPatch), bf = lane_word(rw, kGBf);
   const int64_t t = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(lane_word(rw, kGT + 1))) << 32) |
                                          static_cast<uint32_t>(lane_word(rw, kGT)));
-  const float fw = a.weights ? __builtin_bit_cast(float, lane_word(rw, kGW)) : 1.0f;
+  const float fw = weights ? __builtin_bit_cast(float, lane_word(rw, kGW)) : 1.0f;
   const int32_t ng0 = lane_word(rw, kGNg), ng1 = lane_word(rw, kGNg + 1);
-  const float ws0 = ml.accum_weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs)) : 0.0f;
-  const float ws1 = ml.accum_weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs + 1)) : 0.0f;
+  const float ws0 = weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs)) : 0.0f;
+  const float ws1 = weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs + 1)) : 0.0f;
   VeilWords vw;
   vw.count = static_cast<uint32_t>(lane_word(rw, kVlCount));
   vw.id0 = lane_word(rw, kVlId);
@@ -2311,7 +2331,8 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
       hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
     return fail(PKV_ERR_HIP, "evict_merge: cannot reserve %zu bytes of LDS", smem);
   if (one) {
-    hipLaunchKernelGGL(evict_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u);
+    hipLaunchKernelGGL(evict_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u.states,
+                       u.t_vals, u.weights, u.ml.accum_num_groups, u.ml.accum_weight_sum, u.n_merge, u.MMA, u);
     return check_launch("evict_kernel");
   }
   hipLaunchKernelGGL(update_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u);
