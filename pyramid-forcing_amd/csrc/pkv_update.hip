@@ -511,9 +511,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_prep_kernel(MergeArgs a) 
 // and at the end.
 constexpr int kAccMembersLds = 4096;  // staged member ids per workgroup
 constexpr int kAccBatch = 8;          // member tokens loaded per batch
-constexpr int kAccPreFrames = 4;      // merge frames whose members one thread loads up front
 
-template <bool kPre>
 __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a) {
   __shared__ int32_t s_desc[kMaxMergeFrames][4];
   __shared__ int32_t s_ng[kMaxMergeFrames];
@@ -588,34 +586,10 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
     }
   }
   __syncthreads();
-  // kPre (calls of 2 to kAccPreFrames frames), every merge frame on the
-  // regular grid of 2 x 2 patches (the production Veil groups): each thread
-  // issues the member loads of all its frames at once, so the frames cost one
-  // memory round trip instead of one each.  The additions keep their order.
-  bool pre = kPre && patch == 2 && a.F <= kAccPreFrames;
-  for (int f = 0; f < a.F && pre; ++f) pre = !s_desc[f][0] || s_w[f] > 0;
-
   for (int it = tid; it < kGroupsPerWg * cpt; it += blockDim.x) {
     const int gl = it / cpt, c = (it % cpt) * 8;
     const int g = g0 + gl;
     if (g >= MTPA) break;
-    constexpr int kPreF = kPre ? kAccPreFrames : 1;
-    uint4 fk[kPreF][4], fv[kPreF][4];
-    if (pre) {
-#pragma unroll
-      for (int f = 0; f < kPreF; ++f) {
-        if (f >= a.F || !s_desc[f][0] || g >= s_ng[f]) continue;
-        const int W = s_w[f];
-        const int gcols = W / 2;
-        const int gbase = (g / gcols) * 2 * W + (g % gcols) * 2;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int64_t so = a.src.off(f, h, gbase + (m >> 1) * W + (m & 1)) + c;
-          fk[f][m] = ld16(a.src.k + so);
-          fv[f][m] = ld16(a.src.v + so);
-        }
-      }
-    }
     float ak[8], av[8];
     int cur = -1;  // slot whose accumulators are in registers
     int pos = 0;   // start of the current frame's staged members
@@ -643,7 +617,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
       }
     };
     // one merge frame: slot switch, new-block reset, member additions and
-    // the finalize write (inlined with a constant f in the prefetch loop)
+    // the finalize write
     auto frame = [&](int f) {
       if (!s_desc[f][0]) return;
       const int slot = s_desc[f][1], is_new = s_desc[f][2], fin = s_desc[f][3];
@@ -674,11 +648,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
       const int W = s_w[f];
       const int gcols = W > 0 ? W / patch : 1;
       const int gbase = W > 0 ? (g / gcols) * patch * W + (g % gcols) * patch : 0;
-      if (g < ng && pre) {
-        // the 2 x 2 patch's tokens, loaded above in ascending order
-#pragma unroll
-        for (int m = 0; m < 4; ++m) add_token(fk[f % kPreF][m], fv[f % kPreF][m], w);
-      } else if (g < ng) {
+      if (g < ng) {
         const int m0 = W > 0 ? 0 : s_gs[f][gl], m1 = W > 0 ? patch * patch : s_gs[f][gl + 1];
         const int32_t *gmem = a.ws.members + static_cast<int64_t>(h * a.F + f) * a.FSEQ + s_off[f];
         for (int mb = m0; mb < m1; mb += kAccBatch) {
@@ -717,13 +687,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_accum_kernel(MergeArgs a)
         st16(a.ml.merge_v + (hp * MTPA + g) * D + c, ov);
       }
     };
-    if (pre) {
-#pragma unroll
-      for (int f = 0; f < kPreF; ++f)
-        if (f < a.F) frame(f);
-    } else {
-      for (int f = 0; f < a.F; ++f) frame(f);
-    }
+    for (int f = 0; f < a.F; ++f) frame(f);
     if (cur >= 0) {
       const int64_t ho = static_cast<int64_t>(h) * a.MMA + cur;
       float *pk = a.ml.accum_sum_k + (ho * MTPA + g) * D + c;
@@ -758,12 +722,7 @@ static int merge_prep_smem(const MergeArgs &ma, const void *kernel, size_t &smem
 
 static int launch_merge_accum(const MergeArgs &ma, hipStream_t st) {
   dim3 grid((ma.MTPA + kGroupsPerWg - 1) / kGroupsPerWg, ma.H);
-  // the member prefetch pays where several frames would each cost a memory
-  // round trip; single-frame calls keep the smaller register footprint
-  if (ma.F >= 2 && ma.F <= kAccPreFrames)
-    hipLaunchKernelGGL(merge_accum_kernel<true>, grid, dim3(kMergeThreads), 0, st, ma);
-  else
-    hipLaunchKernelGGL(merge_accum_kernel<false>, grid, dim3(kMergeThreads), 0, st, ma);
+  hipLaunchKernelGGL(merge_accum_kernel, grid, dim3(kMergeThreads), 0, st, ma);
   return check_launch("merge_accum_kernel");
 }
 
