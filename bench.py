@@ -32,7 +32,7 @@ METRIC = "ragged-attn TFLOP/s + cache update/pack GB/s (% roofline); latent chun
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 FSEQ, H, L, D, QTOK = 1560, 12, 30, 128, 4680
-ATTN_KERNEL = "attn_pp_kernel"
+ATTN_KERNEL = "attn_p3_kernel"
 
 # HBM bytes per launch of each workload's dominant kernel, measured with two
 # rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE) and kept, with the

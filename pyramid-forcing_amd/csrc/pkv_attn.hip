@@ -1,8 +1,11 @@
 // Ragged-cache attention for gfx950: bf16 inputs, fp32 online softmax and
 // accumulation, MFMA v_mfma_f32_32x32x16_bf16.  Replaces the reference's
 // flash_attn_varlen_func call (pyramidkv/_mega_cache.py:540-559).
-// head_dim 128 runs attn_pp_kernel (two wave groups alternating between
-// matrix work and data movement, described at the kernel); head_dim 64 runs
+// head_dim 128 runs attn_p3_kernel (384 query rows per workgroup, three
+// wave groups rotating between matrix work, exponentials and data movement)
+// on launches of at least kP3MinGrid of its workgroups, else attn_pp_kernel
+// (256 rows, two groups alternating between matrix work and data
+// movement), both described at the kernel; head_dim 64 runs
 // attn_fwd_kernel, described here.
 //
 // Work decomposition.  A workgroup of 8 waves owns 256 query rows (32 per
@@ -904,6 +907,397 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Three-group kernel (head_dim 128, large launches): attn_p3_kernel
+// ---------------------------------------------------------------------------
+// A workgroup of 12 waves owns 384 query rows (32 per wave) of one (query
+// sequence, head) pair; waves w, w+4 and w+8 share a SIMD (wave w runs on
+// SIMD w % 4), and group g is waves 4g..4g+3, one wave per SIMD.  Each K/V
+// tile copied into LDS feeds 384 query rows: attention at full load runs at
+// a power-limited clock, and moving tiles from L2 into LDS is a large part of
+// its power (timing-only variants of attn_pp_kernel that skip a quarter of
+// the copies ran 12% faster at the same MFMA busy fraction), so the tile
+// feeds as many rows as the register file holds (three waves of at most 168
+// registers per SIMD).  A launch with fewer than kP3MinGrid such workgroups
+// runs attn_pp_kernel instead: its 256-row workgroups put more CUs to work
+// when the grid does not cover the chip several times (one layer's 12 heads
+// in a rollout step are 156 workgroups here, 228 there).
+//
+// Keys stream in tiles of 32.  Each tile takes six barrier-separated
+// intervals; group g runs local interval k of tile t in global interval
+// 6t + k + 2g:
+//
+//   local   work                                        LDS reads
+//   L0      P(t) = exp(S(t)) (mask, row sums)
+//   L1      V(t)^T fragments                                8 KB
+//   L2      O += V(t)^T P(t)                     (8 MFMA)
+//   L3      copy of V(t+3) (groups 0, 1)
+//   L4      K(t+1) fragments; copy of K(t+4) (groups 0, 1) 8 KB
+//   L5      S(t+1) = K(t+1) Q^T                  (8 MFMA)
+//
+// The three groups are in local intervals {0, 2, 4} or {1, 3, 5} at any
+// time, so in every global interval exactly one wave of each SIMD issues
+// matrix instructions, one reads 8 KB of fragments and one computes
+// exponentials or waits.  (Mixing 4 KB of K and 4 KB of V reads in every
+// interval, or splitting the exponentials over two intervals, ran 6% and
+// 13% slower.)
+//
+// The tile copies and the swizzled LDS rows are those of attn_pp_kernel,
+// with the four slots per operand in one 64 KB array.  Groups 0 and 1 copy 4
+// rows each of every tile (two copies per wave per tile) and wait for all
+// but their 4 newest copies at the end of every interval: a copy is complete
+// 12 intervals after it was issued, and every copy is issued at least 15
+// intervals before the first read of its tile and after the reads of the
+// tile its slot held were consumed.  Softmax, the fast / slow pass split and
+// the operand arrangement are those of attn_fwd_kernel.
+constexpr int kP3Waves = 12;
+constexpr int kP3Threads = 64 * kP3Waves;
+constexpr int kP3Rows = 32 * kP3Waves;
+constexpr int kP3MinGrid = 1024;  // workgroups: four per CU
+
+__global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
+  // the eight tile slots (K 0-3, V 4-7) in one 64 KB array at the start of
+  // LDS, so that every fragment read addresses its slot by an immediate
+  // offset; the work-list scratch of the prologue shares it (no copy is
+  // issued before the work list is read)
+  __shared__ __attribute__((aligned(16))) uint16_t kv[8 * kPTileElems];
+  static_assert(8 * kPTileElems * 2 >= 4 * kSchedMax * 4, "work-list scratch fits in the tile slots");
+  int *sched = reinterpret_cast<int *>(kv);
+  auto kslot = [&](auto s) -> uint16_t * { return kv + (decltype(s)::value & 3) * kPTileElems; };
+  auto vslot = [&](auto s) -> uint16_t * { return kv + (4 + (decltype(s)::value & 3)) * kPTileElems; };
+  uint16_t *const Ka = kslot(ic<0>()), *const Kb = kslot(ic<1>()), *const Kc = kslot(ic<2>()), *const Kd = kslot(ic<3>());
+  uint16_t *const Va = vslot(ic<0>()), *const Vb = vslot(ic<1>()), *const Vc = vslot(ic<2>());
+
+  int seq, qt;
+  const int n_seq = p.n_wg / p.q_tiles;
+  if (n_seq <= kSchedMax) {
+    if (!balanced_item(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, kP3Rows, xcd_remap(blockIdx.x, p.n_wg), sched,
+                       seq, qt))
+      return;
+  } else {
+    const int wg = xcd_remap(blockIdx.x, p.n_wg);
+    seq = wg / p.q_tiles;
+    qt = wg % p.q_tiles;
+  }
+  const int b = seq / p.Hq, h = seq % p.Hq;
+  const int q_begin = p.cu_q[b];
+  const int Lq = p.cu_q[b + 1] - q_begin;
+  const int q0 = qt * kP3Rows;
+  if (q0 >= Lq) return;
+  const int kv_idx = p.kv_per_head ? seq : b;
+  const int k_begin = p.cu_k[kv_idx];
+  const int Lk = p.cu_k[kv_idx + 1] - k_begin;
+  const uint16_t *qp = p.q + static_cast<int64_t>(q_begin) * p.q_tok + h * p.q_head;
+  const int64_t kv_off = static_cast<int64_t>(k_begin) * p.kv_tok + (p.kv_per_head ? 0 : h * p.kv_head);
+  const uint16_t *kp = p.k + kv_off;
+  const uint16_t *vp = p.v + kv_off;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int grp = wave_s >> 2, wq = wave_s & 3;
+  const bool copier = grp < 2;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int row_q = q0 + wave * 32 + lq;
+  const bool wave_rows = q0 + wave_s * 32 < Lq;
+  const float c = p.scale_log2;
+
+  bf16x8 qr[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row_q < Lq) v = ldg16(qp + static_cast<int64_t>(row_q) * p.q_tok + 16 * s + 8 * hf);
+    qr[s] = as_bf16x8(v);
+  }
+  // Q is in registers before the first tile copy is issued: the compiler,
+  // which cannot see the copies, then has no load of its own pending in the
+  // key loop, where a wait for one would also wait for every copy in flight
+  wait_vm<0>();
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  const int nT = (Lk + kPK - 1) / kPK;
+
+  // ---- tile copies (groups 0 and 1): buffer resources based at the tile's
+  // first row and bounded at the sequence's last row (rows past the end, and
+  // tiles past the end, copy zeros); this wave copies rows 16*grp + 4*wq ..
+  // +3 of every tile, lane i the 16-byte position i % 16 of row i / 16 of them
+  const int64_t row_elems = p.kv_tok;
+  const int row_bytes = static_cast<int>(row_elems) * 2;
+  const int dma_row = 16 * grp + 4 * wq + (lane >> 4);
+  const int dma_pos = lane & 15;
+  const int k_voff = dma_row * row_bytes + 16 * (dma_pos ^ (dma_row & 15));
+  const int v_voff = dma_row * row_bytes + 16 * (dma_pos ^ (4 * (dma_row & 3)));
+  const int dma_lds = (16 * grp + 4 * wq) * kPRow;
+  // The copies are issued as inline assembly: the compiler then inserts no
+  // wait of its own before the LDS reads of the slots (its bookkeeping
+  // cannot follow the slots around the loop and waits far too early).  Every
+  // wait for them is explicit; the compiler's waits for its own loads stay
+  // correct, since those only ever have more, not fewer, loads after them.
+  auto dma = [&](const uint16_t *base, int kt, uint16_t *slot, int voff) {
+    const int64_t first = static_cast<int64_t>(kt) * kPK;
+    const int64_t left = (static_cast<int64_t>(Lk) - first) * row_elems * 2;
+    const int nrec = static_cast<int>(left <= 0 ? 0 : (left < 0x7fffffff ? left : 0x7fffffff));
+    const uint64_t addr = reinterpret_cast<uint64_t>(base + (left <= 0 ? 0 : first * row_elems));
+    i32x4 rsrc;
+    rsrc[0] = static_cast<int>(addr & 0xffffffffu);
+    rsrc[1] = static_cast<int>((addr >> 32) & 0xffffu);
+    rsrc[2] = nrec;
+    rsrc[3] = kRsrcWord3;
+    const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)slot)) + dma_lds;
+    // m0 is reserved to the compiler, which uses it nowhere else in this
+    // kernel (the listing has no other m0 access)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+  };
+  auto dma_k = [&](uint16_t *slot, int kt) { dma(kp, kt, slot, k_voff); };
+  auto dma_v = [&](uint16_t *slot, int kt) { dma(vp, kt, slot, v_voff); };
+
+  // ---- fragment reads
+  // K: step s reads row lq, 16-byte chunk 2s + hf (swizzled)
+  int kaddr[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) kaddr[s] = lq * kPRow + 16 * ((2 * s + hf) ^ (lq & 15));
+  const int v_row = 4 * hf + ((lane & 15) >> 2);
+  const int v_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int vaddr[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+    vaddr[db] = v_row * kPRow + 16 * ((4 * db + v_col / 8) ^ (4 * (v_row & 3))) + 2 * (v_col % 8);
+  uint4 kreg[8];
+  i16x4 vreg[2][4][2];
+  // K fragments of steps 4*H .. 4*H+3
+  auto load_k_half = [&](const uint16_t *slot, auto h_c) {
+    constexpr int H = decltype(h_c)::value;
+#pragma unroll
+    for (int s = 4 * H; s < 4 * H + 4; ++s)
+      kreg[s] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(slot) + kaddr[s]);
+  };
+  // V^T fragments of key step KS (keys 16*KS .. +15)
+  auto load_v_half = [&](const uint16_t *slot, auto ks_c) {
+    constexpr int KS = decltype(ks_c)::value;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint16_t *ptr =
+          reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(slot) + vaddr[db] + KS * 16 * kPRow);
+      vreg[KS][db][0] = lds_tr16(ptr);
+      vreg[KS][db][1] = lds_tr16(ptr + 8 * kPRow / 2);
+    }
+  };
+  auto gemm0 = [&](f32x16 &acc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kreg[s]), qr[s], acc, 0, 0, 0);
+  };
+  auto gemm1 = [&](const bf16x8 (&pb)[2]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const i16x4 a8[2] = {vreg[ks][db][0], vreg[ks][db][1]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a8), pb[ks], o[db], 0, 0, 0);
+      }
+  };
+  auto mask = [&](f32x16 &s, int kb0) {
+    if (kb0 + kPK > Lk) {
+      asm volatile("");
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (kb0 + 8 * (i / 4) + 4 * hf + (i % 4) >= Lk) s[i] = -INFINITY;
+    }
+  };
+  auto tile_max = [&](const f32x16 &s) {
+    float mq[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mq[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
+    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c;
+  };
+  auto probs = [&](const f32x16 &s, float mr, bf16x8 (&pb)[2]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -mr)));
+    return bf16x8_sum(pb[0], 0.0f) + bf16x8_sum(pb[1], 0.0f);
+  };
+  // end of an interval: this wave's copies older than its 4 newest are
+  // complete, then the workgroup barrier
+  auto step = [&]() {
+    wait_vm<4>();
+    pp_barrier();
+  };
+
+  __shared__ int ovf_any;
+  if (tid == 0) ovf_any = 0;
+  bool ovf = false;
+  if (nT > 0) {
+    // prologue: copies of K0, V0, K1, V1, K2, V2, K3 (the order in which the
+    // loop's tiles -4 .. -1 would have issued them), S(0) and m
+    if (copier) {
+      dma_k(Ka, 0);
+      dma_v(Va, 0);
+      dma_k(Kb, 1);
+      dma_v(Vb, 1);
+      dma_k(Kc, 2);
+      dma_v(Vc, 2);
+      dma_k(Kd, 3);
+    }
+    wait_vm<5>();     // K0 and V0 complete
+    __syncthreads();  // ovf_any initialised
+    f32x16 s;
+    if (wave_rows) {
+      load_k_half(Ka, ic<0>());
+      load_k_half(Ka, ic<1>());
+      gemm0(s);
+      mask(s, 0);
+      m = tile_max(s);  // finite: the first tile holds key 0
+    }
+    // group g runs two intervals behind group g - 1
+    for (int i = 0; i < grp; ++i) {
+      step();
+      step();
+    }
+
+    bf16x8 pb[2];
+    auto iter = [&](auto tt_c, int t) {
+      constexpr int TT = decltype(tt_c)::value;
+      // L0: P(t)
+      mask(s, t * kPK);
+      const float ps = probs(s, m, pb);
+      l += ps;
+      ovf |= !(ps < exp2f(kHeadroom));
+      // the row sums are taken here, not sunk to a later interval where P
+      // would have to stay live
+      asm volatile("" : "+v"(l));
+      step();
+      // L1: V(t) fragments
+      load_v_half(vslot(ic<TT>()), ic<0>());
+      load_v_half(vslot(ic<TT>()), ic<1>());
+      step();
+      // L2: O += V(t)^T P(t)
+      gemm1(pb);
+      step();
+      // L3: copy of V(t+3)
+      if (copier) dma_v(vslot(ic<TT + 3>()), t + 3);
+      step();
+      // L4: K(t+1) fragments, copy of K(t+4)
+      load_k_half(kslot(ic<TT + 1>()), ic<0>());
+      load_k_half(kslot(ic<TT + 1>()), ic<1>());
+      if (copier) dma_k(kslot(ic<TT>()), t + 4);
+      step();
+      // L5: S(t+1)
+      gemm0(s);
+      step();
+    };
+    // waves without query rows (a sequence's last, partial query tile) only
+    // copy their rows of every tile, with the same waits and barriers
+    auto copy_only = [&](auto tt_c, int t) {
+      constexpr int TT = decltype(tt_c)::value;
+      step();
+      step();
+      step();
+      if (copier) dma_v(vslot(ic<TT + 3>()), t + 3);
+      step();
+      if (copier) dma_k(kslot(ic<TT>()), t + 4);
+      step();
+      step();
+    };
+    // a multiple of 4 tiles (the slots cycle with period 4): tiles past the
+    // last copy zero rows and mask every key
+    if (wave_rows) {
+      for (int t0 = 0; t0 < nT; t0 += 4) {
+        iter(ic<0>(), t0);
+        iter(ic<1>(), t0 + 1);
+        iter(ic<2>(), t0 + 2);
+        iter(ic<3>(), t0 + 3);
+      }
+    } else {
+      for (int t0 = 0; t0 < nT; t0 += 4) {
+        copy_only(ic<0>(), t0);
+        copy_only(ic<1>(), t0 + 1);
+        copy_only(ic<2>(), t0 + 2);
+        copy_only(ic<3>(), t0 + 3);
+      }
+    }
+    for (int i = grp; i < 2; ++i) {
+      step();
+      step();
+    }
+    wait_vm<0>();  // no copy may land in LDS after the workgroup ends
+    if (ovf) ovf_any = 1;
+    __syncthreads();
+    if (ovf_any) {
+      // ---- slow pass (a later key outscored the first tile by kHeadroom):
+      // one tile at a time through slots Ka / Va, online softmax with a
+      // moving maximum and O rescaled when it moves
+      m = -INFINITY;
+      l = 0.0f;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+      for (int kt = 0; kt < nT; ++kt) {
+        if (copier) {
+          dma_k(Ka, kt);
+          dma_v(Va, kt);
+        }
+        wait_vm<0>();
+        __syncthreads();
+        if (wave_rows) {
+          // V^T fragments only after the S product (K fragments no longer live)
+          load_k_half(Ka, ic<0>());
+          load_k_half(Ka, ic<1>());
+          f32x16 s2;
+          gemm0(s2);
+          mask(s2, kt * kPK);
+          const float m_new = fmaxf(m, tile_max(s2));
+          const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+          m = m_new;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+          bf16x8 pq[2];
+          l = l * alpha + probs(s2, m, pq);
+          asm volatile("" ::: "memory");
+          load_v_half(Va, ic<0>());
+          load_v_half(Va, ic<1>());
+          gemm1(pq);
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- epilogue: O = O^T / l
+  uint16_t *op = p.o + static_cast<int64_t>(q_begin) * p.o_tok + h * p.o_head;
+  const float lt = half_sum(l);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (row_q < Lq) {
+    uint16_t *orow = op + static_cast<int64_t>(row_q) * p.o_tok;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<__bf16>(o[db][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4 *>(orow + d) = v;
+      }
+  }
+}
+
 template <int D>
 static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   constexpr int BQ = 32 * kWaves;
@@ -912,7 +1306,12 @@ static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   p.cu_q = a->cu_seqlens_q; p.cu_k = a->cu_seqlens_k;
   p.Hq = a->num_heads_q;
   p.kv_per_head = a->kv_per_head;
-  p.q_tiles = (a->max_seqlen_q + BQ - 1) / BQ;
+  // head_dim 128: attn_p3_kernel (384 query rows per workgroup) when its
+  // grid has at least kP3MinGrid workgroups, else attn_pp_kernel
+  const int64_t seqs = static_cast<int64_t>(a->num_batches) * a->num_heads_q;
+  const bool p3 = D == 128 && seqs * ((a->max_seqlen_q + kP3Rows - 1) / kP3Rows) >= kP3MinGrid;
+  const int bq = p3 ? kP3Rows : BQ;
+  p.q_tiles = (a->max_seqlen_q + bq - 1) / bq;
   const int64_t n = static_cast<int64_t>(p.q_tiles) * a->num_batches * a->num_heads_q;
   if (n > 0x7fffffff) return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: grid too large");
   p.n_wg = static_cast<int>(n);
@@ -921,6 +1320,10 @@ static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   p.o_tok = a->o_tok_stride; p.o_head = a->o_head_stride;
   p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   if (p.n_wg == 0) return PKV_OK;
+  if (p3) {
+    hipLaunchKernelGGL(attn_p3_kernel, dim3(p.n_wg), dim3(kP3Threads), 0, st, p);
+    return check_launch("attn_p3_kernel");
+  }
   if (D == 128) {
     hipLaunchKernelGGL(attn_pp_kernel, dim3(p.n_wg), dim3(kThreads), 0, st, p);
     return check_launch("attn_pp_kernel");

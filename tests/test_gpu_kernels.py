@@ -347,6 +347,60 @@ def test_attention_keys_outscoring_the_first_tile_vs_float64():
     assert err.max() < 2e-2 and err.mean() < 2e-3, (err.max(), err.mean())
 
 
+def _attn_check(q, k, v, cu_q, cu_k, B, H, kv_per_head=True):
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    out = torch.full_like(qd, float("nan"))
+    max_q = int(np.diff(cu_q).max())
+    A.ragged_attn_fwd(qd, kd, vd, out, to_dev(cu_q), to_dev(cu_k), B, H, kv_per_head, max_q, 128 ** -0.5)
+    got = O.bf16_to_f32(to_np(out)).astype(np.float64)
+    want = O.ragged_attention_ref(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), cu_q, cu_k, H, kv_per_head)
+    err = np.abs(got - want)
+    assert np.isfinite(got).all()
+    assert err.max() < 2e-2 and err.mean() < 2e-3, (err.max(), err.mean())
+
+
+def _large_launch_case(rng, kv_per_head, B=86, H=12, D=128):
+    """1,032 (sequence, head) pairs: a launch of at least 1,024 workgroups of
+    384 query rows, which runs the 12-wave kernel (smaller launches run the
+    8-wave one).  Query lengths 1-384 with one sequence of 800 (three query
+    tiles: the others' extra tiles exit), key lengths 0-200 with the tile
+    edges (0, 1, 31, 32, 33, 64) among them."""
+    Lq = rng.integers(1, 385, size=B)
+    Lq[:6] = [384, 1, 800, 33, 383, 257]
+    n_kv = B * H if kv_per_head else B
+    Lk = rng.integers(0, 201, size=n_kv)
+    Lk[:8] = [0, 1, 31, 32, 33, 64, 200, 97]
+    cu_q = np.concatenate([[0], np.cumsum(Lq)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(Lk)]).astype(np.int32)
+    q = (rng.standard_normal((cu_q[-1], H, D)) * 0.5).astype(np.float32)
+    kv_shape = (cu_k[-1], D) if kv_per_head else (cu_k[-1], H, D)
+    k = (rng.standard_normal(kv_shape) * 0.5).astype(np.float32)
+    v = (rng.standard_normal(kv_shape) * 0.5).astype(np.float32)
+    return O.f32_to_bf16(q), O.f32_to_bf16(k), O.f32_to_bf16(v), cu_q, cu_k
+
+
+@pytest.mark.parametrize("kv_per_head", [True, False])
+def test_attention_large_launch_vs_float64(kv_per_head):
+    rng = np.random.default_rng(21 + kv_per_head)
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, kv_per_head)
+    _attn_check(q, k, v, cu_q, cu_k, 86, 12, kv_per_head)
+
+
+def test_attention_large_launch_keys_outscoring_the_first_tile_vs_float64():
+    """The 12-wave kernel's slow pass: spiked keys past the first tile score
+    ~130 log2 units above it (past the headroom) in some sequences, ~33
+    (inside it) in others; one spike sits on the last key of a partial tile."""
+    rng = np.random.default_rng(8)
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, True)
+    q[:] = O.f32_to_bf16(np.ones(1, np.float32))[0]
+    lk = np.diff(cu_k)
+    spiked = [s for s in range(len(lk)) if lk[s] > 40][:40]
+    for i, s in enumerate(spiked):
+        pos = lk[s] - 1 if i % 3 == 0 else 35
+        k[cu_k[s] + pos] = O.f32_to_bf16(np.full(128, 8.0 if i % 2 == 0 else 2.0, np.float32))
+    _attn_check(q, k, v, cu_q, cu_k, 86, 12)
+
+
 def test_attention_rejects_causal_and_bad_head_dim():
     q = torch.zeros(4, 1, 128, dtype=torch.bfloat16, device=DEV)
     cu = torch.tensor([0, 4], dtype=torch.int32, device=DEV)
@@ -359,8 +413,7 @@ def test_attention_rejects_causal_and_bad_head_dim():
 
 @pytest.mark.parametrize("F,weighted", [(2, False), (4, False), (4, True)])
 def test_merge_multi_frame_calls_bit_exact(F, weighted):
-    # calls of 2 and 4 frames on the production grid (the accumulation's
-    # path that loads every frame's members at once), offset so that calls
+    # calls of 2 and 4 frames on the production grid, offset so that calls
     # straddle block boundaries: one call finalizes a block and starts the
     # next, in the same or the other slot
     blocks = [[2 + F * b + f for f in range(F)] for b in range(24 // F)]
