@@ -360,11 +360,11 @@ def _attn_check(q, k, v, cu_q, cu_k, B, H, kv_per_head=True):
 
 
 def _large_launch_case(rng, kv_per_head, B=86, H=12, D=128):
-    """1,032 (sequence, head) pairs: a launch of at least 1,024 workgroups of
-    384 query rows, which runs the 12-wave kernel (smaller launches run the
-    8-wave one).  Query lengths 1-384 with one sequence of 800 (three query
-    tiles: the others' extra tiles exit), key lengths 0-200 with the tile
-    edges (0, 1, 31, 32, 33, 64) among them."""
+    """B x H (sequence, head) pairs.  Query lengths 1-384 with one sequence
+    of 800 (three query tiles of 384 rows; the other sequences' extra tiles
+    exit), so the launch has at least 1,024 workgroups and runs the 12-wave
+    kernel (smaller launches run the 8-wave one); key lengths 0-200 with the
+    tile edges (0, 1, 31, 32, 33, 64) among them."""
     Lq = rng.integers(1, 385, size=B)
     Lq[:6] = [384, 1, 800, 33, 383, 257]
     n_kv = B * H if kv_per_head else B
@@ -379,11 +379,13 @@ def _large_launch_case(rng, kv_per_head, B=86, H=12, D=128):
     return O.f32_to_bf16(q), O.f32_to_bf16(k), O.f32_to_bf16(v), cu_q, cu_k
 
 
-@pytest.mark.parametrize("kv_per_head", [True, False])
-def test_attention_large_launch_vs_float64(kv_per_head):
-    rng = np.random.default_rng(21 + kv_per_head)
-    q, k, v, cu_q, cu_k = _large_launch_case(rng, kv_per_head)
-    _attn_check(q, k, v, cu_q, cu_k, 86, 12, kv_per_head)
+@pytest.mark.parametrize("kv_per_head,H", [(True, 12), (False, 12), (True, 11)])
+def test_attention_large_launch_vs_float64(kv_per_head, H):
+    # 86 x 12 = 1,032 pairs exceed the 1,024 that the XCD-balanced work list
+    # ranks (plain work order); 86 x 11 = 946 take the balanced order
+    rng = np.random.default_rng(21 + kv_per_head + H)
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, kv_per_head, H=H)
+    _attn_check(q, k, v, cu_q, cu_k, 86, H, kv_per_head)
 
 
 def test_attention_large_launch_keys_outscoring_the_first_tile_vs_float64():
