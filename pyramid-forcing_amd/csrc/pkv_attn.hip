@@ -939,8 +939,8 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
 // time, so in every global interval exactly one wave of each SIMD issues
 // matrix instructions, one reads 8 KB of fragments and one computes
 // exponentials or waits.  (Mixing 4 KB of K and 4 KB of V reads in every
-// interval, or splitting the exponentials over two intervals, ran 6% and
-// 13% slower.)
+// interval ran 6% slower; moving half of the exponentials beside the V^T
+// reads, 10% slower.)
 //
 // The tile copies and the swizzled LDS rows are those of attn_pp_kernel,
 // with the four slots per operand in one 64 KB array.  Groups 0 and 1 copy 4
