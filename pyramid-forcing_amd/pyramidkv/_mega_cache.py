@@ -27,6 +27,12 @@ import torch
 
 from . import _mega_state_ops, _mega_state_ref as ref, _ops
 from .base import HeadComposition
+from .cyclic import CyclicStrategy
+from .lag import LagStrategy
+from .merge import MergeStrategy
+from .stride import StrideStrategy
+
+_STRATEGY_TYPES = {c.__name__: c for c in (CyclicStrategy, StrideStrategy, LagStrategy, MergeStrategy)}
 
 _STRATEGY_NAME_TO_KIND = {"RecentStrategy": ref.SK_RECENT, "CyclicStrategy": ref.SK_CYCLIC,
                           "StrideStrategy": ref.SK_STRIDE, "LagStrategy": ref.SK_LAG, "MergeStrategy": ref.SK_MERGE}
@@ -193,28 +199,19 @@ class MegaCache:
 
 
 def _composition_to_perhead_state(composition: HeadComposition) -> ref.PerHeadState:
-    """HeadComposition -> state record (reference _mega_cache.py:572-628)."""
+    """HeadComposition -> state record (reference _mega_cache.py:572-628): the
+    first middle strategy's record (one strategy kind per head), chosen by
+    the strategy's class name as the reference does, so any object with those
+    attributes and one of those names encodes the same way; no or an unknown
+    strategy: sink + recent only.  The composition's sink frames become the
+    record's sink capacity."""
     sink_cap = int(getattr(composition, "sink_frames", 0))
-    if not composition.middle_strategies:
-        s = ref.make_recent()
-        s.sink_capacity = sink_cap
-        return s
-    mid = composition.middle_strategies[0]
-    name = type(mid).__name__
-    if name == "CyclicStrategy":
-        s = ref.make_cyclic(int(mid.period), int(mid.bucket_cap))
-    elif name == "StrideStrategy":
-        cap = int(mid.capacity)
-        if cap <= 0 or cap > ref.MAX_T_KEYED:
-            cap = ref.MAX_T_KEYED
-        s = ref.make_stride(int(mid.interval), cap)
-    elif name == "LagStrategy":
-        hist = min(int(getattr(mid, "history_frames", ref.MAX_T_KEYED)), ref.MAX_T_KEYED)
-        s = ref.make_lag(hist, list(getattr(mid, "offsets", []) or []))
-    elif name == "MergeStrategy":
-        s = ref.make_merge(int(getattr(mid, "patch_size", 2)), int(getattr(mid, "capacity", ref.MAX_MERGE_BLOCKS)))
-    else:
-        s = ref.make_recent()
+    s = ref.make_recent()
+    if composition.middle_strategies:
+        mid = composition.middle_strategies[0]
+        cls = _STRATEGY_TYPES.get(type(mid).__name__)
+        if cls is not None:
+            s = cls.state_record(mid)
     s.sink_capacity = sink_cap
     return s
 

@@ -28,9 +28,17 @@ class FrameAnchor:
 
 class MiddleStrategy:
     """Base of the middle-segment parameter records.  ``dynamic_rope``: the
-    frames' temporal RoPE index is remapped at readout."""
+    frames' temporal RoPE index is remapped at readout.
+
+    ``state_record()`` encodes the strategy into the per-head state record
+    that the device state machine and planner read (the reference's
+    _mega_cache.py:572-628 translation, one strategy kind per head); it
+    raises ValueError when the parameters do not fit the record's bounds."""
 
     dynamic_rope: bool = True
+
+    def state_record(self):
+        raise NotImplementedError(f"{type(self).__name__} has no state-record encoding")
 
 
 class HeadComposition:

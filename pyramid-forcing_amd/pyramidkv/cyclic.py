@@ -5,6 +5,7 @@ Frame t falls in phase t % period; each phase keeps a ring of
 the ring in the per-head state record."""
 from __future__ import annotations
 
+from . import _mega_state_ref as ref
 from .base import MiddleStrategy
 
 
@@ -13,3 +14,8 @@ class CyclicStrategy(MiddleStrategy):
         self.period = max(1, int(period))
         self.bucket_cap = max(1, int(bucket_cap))
         self.dynamic_rope = bool(dynamic_rope)
+
+    def state_record(self) -> ref.PerHeadState:
+        """Wave record: the phase ring of period x bucket_cap slots (at most
+        MAX_PHASE x MAX_BUCKET); slot i of phase q is middle slot q * MAX_BUCKET + i."""
+        return ref.make_cyclic(int(self.period), int(self.bucket_cap))

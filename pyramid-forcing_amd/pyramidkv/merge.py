@@ -6,6 +6,7 @@ the builder's default).  The accumulation runs on the device
 (``merge_accum_kernel``)."""
 from __future__ import annotations
 
+from . import _mega_state_ref as ref
 from .base import MiddleStrategy
 
 
@@ -18,3 +19,9 @@ class MergeStrategy(MiddleStrategy):
     @property
     def block_frames(self) -> int:
         return self.patch_size * self.patch_size
+
+    def state_record(self) -> ref.PerHeadState:
+        """Veil record: blocks of patch_size**2 frames (at most
+        MAX_MERGE_BLOCK_FRAMES), capacity finalized anchors (1 to
+        MAX_MERGE_BLOCKS; the builder's -1 is rejected, as in the reference)."""
+        return ref.make_merge(int(getattr(self, "patch_size", 2)), int(getattr(self, "capacity", ref.MAX_MERGE_BLOCKS)))

@@ -14,7 +14,7 @@ from pyramidkv import _mega_state_ops as S
 from pyramidkv import _mega_state_ref as R
 from pyramidkv import _ops, factory
 from pyramidkv._mega_cache import _composition_to_perhead_state
-from pyramidkv import CyclicStrategy, HeadComposition, LagStrategy, MergeStrategy, StrideStrategy
+from pyramidkv import CyclicStrategy, HeadComposition, LagStrategy, MergeStrategy, RecentStrategy, StrideStrategy
 from pyramidkv.rope import flat_freq_parts, map_dynamic_pos_time, map_sink_time, wan_freqs
 
 
@@ -87,6 +87,37 @@ def test_composition_to_state_edge_cases():
     assert st.kind == R.SK_LAG and st.capacity == R.MAX_T_KEYED
     first = HeadComposition("c", -1, 1, 4, [CyclicStrategy(6, 2), MergeStrategy(2, 4)])
     assert _composition_to_perhead_state(first).kind == R.SK_CYCLIC
+
+
+def test_strategy_state_records():
+    """Each strategy encodes its own record; bounds as the reference's
+    make_* helpers check them (_mega_state_ref.py)."""
+    st = CyclicStrategy(3, 4).state_record()
+    assert (st.kind, st.period, st.bucket_cap) == (R.SK_CYCLIC, 3, 4)
+    with pytest.raises(ValueError, match="cyclic period"):
+        CyclicStrategy(6, 5).state_record()  # 30 slots > the 6 x 4 ring
+    assert StrideStrategy(6, 30).state_record().capacity == R.MAX_T_KEYED
+    assert (StrideStrategy(4, 5).state_record().interval, StrideStrategy(4, 5).state_record().capacity) == (4, 5)
+    st = LagStrategy([12, 6, 6, 3], history_frames=10).state_record()
+    assert (st.kind, st.capacity, st.lag_offset_count, list(st.lag_offsets[:3])) == (R.SK_LAG, 10, 3, [3, 6, 12])
+    st = MergeStrategy(2, 4).state_record()
+    assert (st.kind, st.patch_size, st.block_frames, st.capacity) == (R.SK_MERGE, 2, 4, 4)
+    with pytest.raises(ValueError, match="merge needs"):
+        MergeStrategy(3, 4).state_record()  # 9-frame blocks > 4
+    with pytest.raises(ValueError, match="merge needs"):
+        MergeStrategy(2, -1).state_record()
+    assert RecentStrategy().state_record().kind == R.SK_RECENT
+
+
+def test_composition_dispatches_on_the_strategy_class_name():
+    """The reference picks the encoding by the strategy's class name, so an
+    object of another class with that name and those attributes encodes the
+    same way; an unknown middle strategy means sink + recent only."""
+    Foreign = type("StrideStrategy", (), {"interval": 3, "capacity": 7})
+    st = _composition_to_perhead_state(HeadComposition("f", 1, 2, 4, [Foreign()]))
+    assert (st.kind, st.interval, st.capacity, st.sink_capacity) == (R.SK_STRIDE, 3, 7, 2)
+    Other = type("Unknown", (), {})
+    assert _composition_to_perhead_state(HeadComposition("u", 1, 2, 4, [Other()])).kind == R.SK_RECENT
 
 
 def test_policy_compiler_rejects_ambiguous_maps():
