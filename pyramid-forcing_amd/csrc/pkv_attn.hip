@@ -946,9 +946,10 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
 // with the four slots per operand in one 64 KB array.  Groups 0 and 1 copy 4
 // rows each of every tile (two copies per wave per tile) and wait for all
 // but their 4 newest copies at the end of every interval: a copy is complete
-// 12 intervals after it was issued, and every copy is issued at least 15
-// intervals before the first read of its tile and after the reads of the
-// tile its slot held were consumed.  Softmax, the fast / slow pass split and
+// 12 intervals after it was issued, and every copy is issued at least 14
+// intervals before the first read of its tile (group 1's V copy at global
+// 6t+5, V(t+3) first read at 6t+19) and after the reads of the tile its slot
+// held were consumed.  Softmax, the fast / slow pass split and
 // the operand arrangement are those of attn_fwd_kernel.
 constexpr int kP3Waves = 12;
 constexpr int kP3Threads = 64 * kP3Waves;
