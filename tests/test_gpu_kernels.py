@@ -388,6 +388,27 @@ def test_attention_large_launch_vs_float64(kv_per_head, H):
     _attn_check(q, k, v, cu_q, cu_k, 86, H, kv_per_head)
 
 
+def test_attention_large_launch_strided_views_vs_float64():
+    """Q, K, V and O as the first 128 columns of 256-wide rows (token and head
+    strides of the views, K/V rows 512 bytes apart): the 12-wave kernel reads
+    and writes through the strides and leaves the other columns untouched."""
+    rng = np.random.default_rng(31)
+    B, H = 86, 12
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, True, B=B, H=H)
+    wide = lambda a: np.concatenate([a, np.zeros(a.shape, np.uint16)], axis=-1)
+    qw, kw, vw = to_dev(wide(q)), to_dev(wide(k)), to_dev(wide(v))
+    qd, kd, vd = qw[..., :128], kw[..., :128], vw[..., :128]
+    ow = torch.full_like(qw, float("nan"))
+    out = ow[..., :128]
+    A.ragged_attn_fwd(qd, kd, vd, out, to_dev(cu_q), to_dev(cu_k), B, H, True, int(np.diff(cu_q).max()), 128 ** -0.5)
+    got = O.bf16_to_f32(to_np(out)).astype(np.float64)
+    want = O.ragged_attention_ref(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), cu_q, cu_k, H, True)
+    err = np.abs(got - want)
+    assert np.isfinite(got).all()
+    assert err.max() < 2e-2 and err.mean() < 2e-3, (err.max(), err.mean())
+    assert torch.isnan(ow[..., 128:]).all()
+
+
 def test_attention_large_launch_keys_outscoring_the_first_tile_vs_float64():
     """The 12-wave kernel's slow pass: spiked keys past the first tile score
     ~130 log2 units above it (past the headroom) in some sequences, ~33
