@@ -1257,6 +1257,22 @@ __device__ inline int merge_head_at(const UpdArgs &a, int i) {
   return __builtin_ctzll(m);
 }
 
+// Token tiles in grid order: the heads without Veil merges first, then the
+// Veil heads (whose token tiles stage no record and write no middle copies),
+// so that the tiles left for the grid's last dispatch round are the short
+// ones.  Position i -> head, ascending within each part.
+__device__ inline int token_head_at(const UpdArgs &a, int i) {
+  if (a.n_mh == 0) return i;
+  const int n0 = a.H - a.n_mh;
+  if (i >= n0) return merge_head_at(a, i - n0);
+  const int hl = min(a.H, 63);
+  uint64_t m = ~a.merge_heads & ((uint64_t{1} << hl) - 1);
+  const int low = __popcll(m);
+  if (i >= low) return 63 + (i - low);  // heads >= 63 without merges (bit 63 clear)
+  for (int k = 0; k < i; ++k) m &= m - 1;
+  return __builtin_ctzll(m);
+}
+
 __device__ inline int arrive_take(const UpdArgs &a, int h, int idx) {
   return atomicAdd(arrive_counters(a, h) + (idx % kArriveFan) * kArriveStride, 1);
 }
@@ -1541,7 +1557,7 @@ __global__ void __launch_bounds__(kUpdThreads) update_kernel(UpdArgs a) {
   const int b = blockIdx.x;
   const int n_mt = a.n_mh * a.n_merge;
   const bool merge_tile = b < n_mt;
-  const int h = merge_tile ? merge_head_at(a, b / a.n_merge) : (b - n_mt) / a.n_scat;
+  const int h = merge_tile ? merge_head_at(a, b / a.n_merge) : token_head_at(a, (b - n_mt) / a.n_scat);
   const int tile = merge_tile ? b % a.n_merge : (b - n_mt) % a.n_scat;
   int ticket = 0;  // thread 0: the arrival sub-counter's previous value
   if (merge_tile)
