@@ -469,13 +469,6 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_rows[kPackTok][3];
   const int items = a.n_seg * a.tiles_per_seg;
   const int cpt = a.D / 8;
-  // when cpt divides the block, a thread handles one chunk index of every
-  // token it touches, so its 4 table entries are resolved once
-  const bool fixed_chunk = (kPackThreads % cpt) == 0;
-  PairTab tabs[4];
-  if (a.fuse && fixed_chunk)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tabs[e] = pair_tab(threadIdx.x % cpt, e, a.rope);
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int seg = it / a.tiles_per_seg, tile = it % a.tiles_per_seg;
     // every descriptor field is read before the first test, by scalar loads
@@ -541,14 +534,10 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
           uint4 k4 = kk[u];
           if (rope) {
             const int rows[3] = {s_rows[tl][0], s_rows[tl][1], s_rows[tl][2]};
-            if (fixed_chunk) {
-              k4 = rope_chunk_rows(k4, tabs, rows);
-            } else {
-              PairTab t4[4];
+            PairTab t4[4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) t4[q] = pair_tab(ch, q, a.rope);
-              k4 = rope_chunk_rows(k4, t4, rows);
-            }
+            for (int q = 0; q < 4; ++q) t4[q] = pair_tab(ch, q, a.rope);
+            k4 = rope_chunk_rows(k4, t4, rows);
           }
           st16_nt(ok + e, k4);
           st16_nt(ov + e, vv[u]);
