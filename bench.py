@@ -7,10 +7,12 @@ BASELINE workload "config 2": 30 layers x 12 heads, head_dim 128, bf16,
 {-1, 1, 2} (Wave 10 frames, Anchor 0-12 frames, Veil 6 frames; 1 frame =
 1,560 tokens; capped at 21 frames).  One step = one launch of the ragged
 attention kernel over all 360 (layer, head) sequences, inputs resident in
-HBM.  The "secondary" object reports config 3 (30-layer cache update +
-plan + pack at step 40, HBM GB/s) and config 4 (Veil merge accumulate,
-HBM GB/s), each with a bit-exact check against the CPU oracle and the
-oracle's own throughput as the CPU baseline.
+HBM.  The "secondary" object reports config 1 (the single-layer step:
+update, plan + pack with RoPE, query RoPE, attention), config 3 (30-layer
+cache update + plan + pack at step 40, HBM GB/s), config 4 (Veil merge
+accumulate, HBM GB/s) and config 5 (the causal DiT rollout), each with a
+check against the CPU oracle and the oracle's own throughput as the CPU
+baseline where the config has one.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 Prints one JSON line.
@@ -193,6 +195,185 @@ def cpu_baseline_attention(r, max_seqs: int = 8, runs: int = 5):
 # ---------------------------------------------------------------------------
 MAX_SINK, MAX_MIDDLE, MAX_RECENT, MAX_CHUNKS = 3, 24, 4, 8
 ROW = D * 2  # bytes of one bf16 K or V row
+
+
+# ---------------------------------------------------------------------------
+# config 1: the single-layer step (sink 1 + recent 3 frames, chunk t = 18..20)
+# ---------------------------------------------------------------------------
+C1_T0, C1_F, C1_W = 18, 3, 52
+
+
+def bench_config1(steps: int, warmup: int, seed: int = 0):
+    """BASELINE config 1 at full size on the GPU: 12 heads x head_dim 128,
+    every head sink 1 frame + recent 3 frames, no middle.  Frame 0 sits in
+    the sink; one step scatters the new 3-frame chunk (t = 18, 19, 20) into
+    the recent window (clean pass), builds the 3-chunk plan and packs
+    sink + recent with the 3D RoPE at remapped times (sink t -> 0 by
+    window_clamp(18, 21)), rotates the queries at their own positions, and
+    runs the non-causal attention of each query frame over its 6,240 keys
+    (36 sequences of 1,560 x 6,240; 179.4 GFLOP).  This is the step
+    MegaCache.update + MegaCache.attend perform (reference
+    pyramidkv/_mega_cache.py:136-569, CPU RoPE pyramidkv/rope.py:18-68).
+    Each phase is bracketed by HIP events on the launch stream; the cache's
+    counters and state are restored before every step."""
+    import numpy as np
+    import torch
+
+    from pyramidkv import _ops, factory
+    from pyramidkv._mega_cache import build_mega_caches
+    from pyramidkv.base import HeadComposition
+    from pyramidkv.rope import wan_freqs
+
+    dev = "cuda:0"
+    F, T0, W = C1_F, C1_T0, C1_W
+    comps = [[HeadComposition(f"h{h}", 0, sink_frames=1, recent_frames=3) for h in range(H)]]
+    cache = build_mega_caches(1, H, D, FSEQ, 1, 1, 3, comps, max_attend_chunks=F, device=dev, freqs=wan_freqs(D),
+                              spatial_width=W, spatial_height=FSEQ // W, **factory.PYRAMID_FORCING_REMAP)[0]
+    ctx, mgr, ops = cache.ctx, cache.ctx.mgr, _ops.ops()
+    rng = np.random.default_rng(seed)
+    draw = lambda n: rng.standard_normal((n, H, D)).astype(np.float32)
+    k0, v0 = draw(FSEQ), draw(FSEQ)
+    k, v, q = draw(F * FSEQ), draw(F * FSEQ), draw(F * FSEQ)
+    bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16).view(1, a.shape[0], H, D)
+    cache.update(bf(k0), bf(v0), 0, cache_update_mode="clean")
+    start = T0 * FSEQ
+    nk, nv, nq = bf(k), bf(v), bf(q)
+    tok = np.arange(F * FSEQ)
+    qpos = np.stack([T0 + tok // FSEQ, (tok % FSEQ) // W, tok % W], axis=1).astype(np.int64)
+    qpos_rows = torch.from_numpy(np.repeat(qpos, H, axis=0)).to(dev)
+    cu_q = torch.arange(0, F * FSEQ + 1, FSEQ, dtype=torch.int32, device=dev)
+    snap_src = [ctx.states_bytes, mgr.valid_count(), ctx.committed_vc]
+    snap = [t.clone() for t in snap_src]
+    kf, vf = mgr.k_flat_out().view(-1, D), mgr.v_flat_out().view(-1, D)
+    res = {}
+
+    def step(ev=None):
+        mark = (lambda i: ev[i].record()) if ev else (lambda i: None)
+        mark(0)
+        cache.update(nk, nv, start, cache_update_mode="clean")
+        mark(1)
+        cu_k = cache.attend_kv(start, F)
+        mark(2)
+        q_rot = ops.rope_apply(nq.view(-1, D), qpos_rows, *ctx.freq_parts_flat)
+        mark(3)
+        res["out"] = _ops.ragged_attention(q_rot.view(F * FSEQ, H, D), kf, vf, cu_q, cu_k, FSEQ, None,
+                                           kv_per_head=True)
+        mark(4)
+        res["cu_k"], res["q_rot"] = cu_k, q_rot
+
+    for _ in range(max(1, warmup)):
+        _restore(snap_src, snap)
+        step()
+    torch.cuda.synchronize()
+    phases = []
+    for _ in range(steps):
+        _restore(snap_src, snap)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        step(ev)
+        torch.cuda.synchronize()
+        phases.append([ev[i].elapsed_time(ev[i + 1]) for i in range(4)])
+    ph = np.median(np.asarray(phases), axis=0)
+    total = int(res["cu_k"][-1].item())
+    lk = F * FSEQ + FSEQ
+    flops = 4.0 * F * H * FSEQ * lk * D
+    n_new = F * H * FSEQ
+    upd_bytes = n_new * 2 * ROW + n_new * (2 * ROW + 24)  # read new K/V once, write recent K/V/pos
+    pack_bytes = total * (2 * ROW + 2 * ROW + 48)
+    rope_bytes = F * FSEQ * H * (ROW + ROW + 24)
+    return dict(cache=cache, start=start, k0=k0, v0=v0, k=k, v=v, q=q, qpos=qpos, res=res, total=total, flops=flops,
+                phase_ms=[float(x) for x in ph], step_ms=float(np.median([sum(p) for p in phases])),
+                upd_bytes=upd_bytes, pack_bytes=pack_bytes, rope_bytes=rope_bytes)
+
+
+def config1_cpu_and_parity(r, runs: int = 5):
+    """The oracle's restatement of the same config-1 step on the host, timed
+    `runs` times (median): MegaCacheRef.update of the chunk (numpy), the
+    3-chunk plan (C) and the pack with RoPE (C, segments split over all host
+    threads), the query RoPE (C, rows split over the threads) and float32
+    softmax attention of the 36 (chunk, head) sequences (numpy; its matrix
+    products use BLAS on every host thread).  The inputs are the GPU's own,
+    rounded to bf16 as the device pools hold them.  The first run's packed
+    K/V/pos are compared bit for bit with the GPU's, and its attention output
+    with the GPU's at the north star's tolerance (max-abs 2e-2, mean-abs
+    2e-3)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    F, T0 = C1_F, C1_T0
+    cache, mgr = r["cache"], r["cache"].ctx.mgr
+    bf16 = lambda a: O.f32_to_bf16(a)
+    k0, v0, k, v, q = (bf16(r[n]) for n in ("k0", "v0", "k", "v", "q"))
+    tables = O.rope_tables(D)
+    g = O.Geometry(1, H, D, FSEQ, 1, 1, 3, max_attend_chunks=F)
+    host = lambda t: (t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+                      if t.dtype == torch.bfloat16 else t.detach().contiguous().cpu().numpy())
+    states0 = host(cache.ctx.states_bytes).reshape(1, -1).copy()
+    caps = host(cache.ctx.sink_caps_per_head)
+    rm = factory_remap()
+    qpos_rows = np.repeat(r["qpos"], H, axis=0)
+    q_rows = q.reshape(-1, D)
+    nthr = host_threads()
+    cu_q = np.arange(0, F * FSEQ + 1, FSEQ)
+
+    def one(pool):
+        ref = O.MegaCacheRef(g, states0, caps, spatial_width=C1_W, sink_mode=rm[0], cmin=rm[1], cmax=rm[2],
+                             lag=rm[3], tables=tables)
+        ref.update(0, k0, v0, 0, "clean")  # frame 0 into the sink (set-up, as on the GPU)
+        t0 = time.perf_counter()
+        ref.update(0, k, v, r["start"], "clean")
+        t_list = [T0 + c for c in range(F)]
+        cu, sk, sg, sl, dst, _tr, trm, tot = O.plan_multi(g, ref.states[0], ref.valid_count[0],
+                                                          ref.merge_token_count[0], t_list, *ref.remap)
+        sga = O.layer_offset_slot_global(sg, sk, 0, g)
+        out = (np.zeros((tot, D), np.uint16), np.zeros((tot, D), np.uint16), np.zeros((tot, 3), np.int64))
+        cuts = np.linspace(0, len(sk), 4 * nthr + 1).astype(int)
+        list(pool.map(lambda i: O.pack(ref.pools(), g, sk[cuts[i]:cuts[i + 1]], sga[cuts[i]:cuts[i + 1]],
+                                       sl[cuts[i]:cuts[i + 1]], dst[cuts[i]:cuts[i + 1]], trm[cuts[i]:cuts[i + 1]],
+                                       tables, capacity=tot, out=out), range(len(cuts) - 1)))
+        rc = np.linspace(0, q_rows.shape[0], nthr + 1).astype(int)
+        parts = list(pool.map(lambda i: O.rope_apply(q_rows[rc[i]:rc[i + 1]], qpos_rows[rc[i]:rc[i + 1]], tables),
+                              range(nthr)))
+        q_rot = np.concatenate(parts).reshape(F * FSEQ, H, D)
+        qf = O.bf16_to_f32(q_rot)
+        kf, vf = O.bf16_to_f32(out[0]), O.bf16_to_f32(out[1])
+        att = np.zeros((F * FSEQ, H, D), np.float32)
+        for c in range(F):
+            for h in range(H):
+                s_ = c * H + h
+                att[cu_q[c]:cu_q[c + 1], h] = O.attention_ref(qf[cu_q[c]:cu_q[c + 1], h], kf[cu[s_]:cu[s_ + 1]],
+                                                              vf[cu[s_]:cu[s_ + 1]], D ** -0.5, dtype=np.float32)
+        return time.perf_counter() - t0, (cu, tot, out, att)
+
+    secs, first = [], None
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=nthr) as pool:
+        for i in range(runs):
+            dt, res = one(pool)
+            secs.append(dt)
+            if i == 0:
+                first = res
+    cu, tot, (pk, pv, pp), att = first
+    res = r["res"]
+    packed_ok = (tot == r["total"] and np.array_equal(cu, host(res["cu_k"]))
+                 and np.array_equal(pk, host(mgr.k_flat_out()).reshape(-1, D)[:tot])
+                 and np.array_equal(pv, host(mgr.v_flat_out()).reshape(-1, D)[:tot])
+                 and np.array_equal(pp, host(mgr.pos_flat_out())[:tot]))
+    got = res["out"].float().cpu().numpy()
+    err = np.abs(got.astype(np.float64) - att.astype(np.float64))
+    med = float(np.median(secs))
+    cpu = dict(value=round(r["flops"] / med / 1e12, 4), unit="TFLOP/s", step_s=round(med, 4), cores=nthr, kind="port",
+               host_cpu=host_cpu(),
+               sample=f"the whole config-1 step (update, 3-chunk plan, pack with RoPE, query RoPE, float32 attention "
+                      f"of 36 sequences of 1560 x {FSEQ * (F + 1)}) by the oracle's restatement on {nthr} host "
+                      f"threads; median of {runs} runs ({', '.join(f'{x:.2f}' for x in secs)} s); value = the "
+                      f"step's attention flop / step time")
+    parity = dict(packed_kv_pos_bit_exact=bool(packed_ok), attn_max_abs=round(float(err.max()), 6),
+                  attn_mean_abs=round(float(err.mean()), 7), tolerance=[2e-2, 2e-3],
+                  ok=bool(packed_ok and err.max() < 2e-2 and err.mean() < 2e-3),
+                  reference="oracle: bit-exact pack, float32 softmax attention")
+    return cpu, parity
 
 
 def _restore(dst, src):
@@ -406,15 +587,19 @@ def bench_merge(steps: int, warmup: int, seed: int = 0):
     import torch
 
     from oracle import oracle as O
-    from pyramidkv import _ops
+    from pyramidkv import _mega_state_ops, _mega_state_ref, _ops
 
     ops = _ops.ops()
     dev = "cuda:0"
     rng = np.random.default_rng(seed)
     MMA, MMB, MT = 2, 6, 420
-    states0 = O.states_to_bytes([O.make_merge(2, 6) for _ in range(H)]).view(np.uint8).reshape(-1)
-    k_np = O.f32_to_bf16(rng.standard_normal((EVICTIONS, 1, H, FSEQ, D)).astype(np.float32))
-    v_np = O.f32_to_bf16(rng.standard_normal((EVICTIONS, 1, H, FSEQ, D)).astype(np.float32))
+    # inputs from the package's own builders: Veil records (patch 2, 6
+    # completed anchors) and bf16 frames; the oracle gets the same bits
+    states0 = _mega_state_ops.pack_states([_mega_state_ref.make_merge(2, 6) for _ in range(H)])
+    states0 = np.ascontiguousarray(states0).view(np.uint8).reshape(-1)
+    bits = lambda a: torch.from_numpy(a).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    k_np = bits(rng.standard_normal((EVICTIONS, 1, H, FSEQ, D)).astype(np.float32))
+    v_np = bits(rng.standard_normal((EVICTIONS, 1, H, FSEQ, D)).astype(np.float32))
     w_np = rng.uniform(0.1, 1.0, size=EVICTIONS).astype(np.float32)
     pos_np = np.zeros((EVICTIONS, 1, H, FSEQ, 3), np.int64)
     tok = np.arange(FSEQ)
@@ -561,7 +746,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true", help="skip the config-3 / 4 / 5 measurements")
     ap.add_argument("--e2e-chunks", type=int, default=E2E_CHUNKS, help="3-frame chunks of the config-5 rollout")
-    ap.add_argument("--workload", choices=["all", "attn", "cache", "merge", "e2e", "copy"], default="all",
+    ap.add_argument("--workload", choices=["all", "attn", "config1", "cache", "merge", "e2e", "copy"], default="all",
                     help="run one workload alone and print its timing (for profiler runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -623,6 +808,9 @@ def single_workload(args):
     if args.workload == "merge":
         c4 = bench_merge(args.steps, args.warmup)
         return {"workload": "merge", "ms": c4["ms"], "bytes_per_step": c4["bytes"]}
+    if args.workload == "config1":
+        c1 = bench_config1(args.steps, args.warmup)
+        return {"workload": "config1", "step_ms": c1["step_ms"], "phase_ms": c1["phase_ms"], "flop": c1["flops"]}
     if args.workload == "e2e":
         return {"workload": "e2e", **bench_e2e(args.e2e_chunks)}
     src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
@@ -633,9 +821,43 @@ def single_workload(args):
     return {"workload": "copy", "bytes_read_per_launch": src.numel() * 2, "bytes_written_per_launch": dst.numel() * 2}
 
 
+def config1_entry(args):
+    """secondary.config1_single_layer_step: GPU phases, rooflines of the
+    attention (MFMA) and of the pack (HBM), the oracle's CPU step."""
+    import torch
+    r = bench_config1(args.steps, args.warmup)
+    up_ms, pk_ms, rq_ms, at_ms = r["phase_ms"]
+    at_tf = r["flops"] / (at_ms * 1e-3) / 1e12
+    pk_gbs = r["pack_bytes"] / (pk_ms * 1e-3) / 1e9
+    step_tf = r["flops"] / (r["step_ms"] * 1e-3) / 1e12
+    entry = {
+        "value": round(step_tf, 2), "unit": "TFLOP/s", "ms_per_step": round(r["step_ms"], 4),
+        "value_definition": "attention flop of the step / whole step time (update + plan + pack + query RoPE + "
+                            "attention)",
+        "workload": "config1_single_layer_step", "heads": H, "head_dim": D, "frame_tokens": FSEQ,
+        "query_tokens": C1_F * FSEQ, "keys_per_query_frame": FSEQ * (C1_F + 1), "chunk_t": [C1_T0, C1_T0 + C1_F - 1],
+        "policy": "every head sink 1 + recent 3 frames", "flop_per_step": r["flops"],
+        "phases_ms": {"update": round(up_ms, 4), "plan_pack_rope": round(pk_ms, 4), "query_rope": round(rq_ms, 4),
+                      "attention": round(at_ms, 4)},
+        "bytes": {"update": r["upd_bytes"], "pack": r["pack_bytes"], "query_rope": r["rope_bytes"]},
+        "roofline": {"bound": "mfma", "achieved": round(at_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(at_tf / PEAK_BF16_TFLOPS, 4), "traffic": None, "kernel": "attn_pp_kernel",
+                     "avg_launch_ms": round(at_ms, 4)},
+        "roofline_pack": {"bound": "hbm", "achieved": round(pk_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(pk_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                          "kernel": "plan_kernel + pack_kernel", "avg_ms": round(pk_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        cpu, parity = config1_cpu_and_parity(r)
+        entry["cpu_baseline"], entry["parity"] = cpu, parity
+    del r
+    torch.cuda.empty_cache()
+    return entry
+
+
 def secondary(args):
     import torch
-    out = {}
+    out = {"config1_single_layer_step": config1_entry(args)}
     c3 = bench_cache_step(args.steps, args.warmup)
     ms = c3["graph_ms"] if c3["graph_ms"] is not None else c3["eager_ms"]
     gbs = c3["total_bytes"] / (ms * 1e-3) / 1e9

@@ -122,7 +122,11 @@ int pkv_state_update(uint8_t *states, int32_t num_heads,
 
 /* pyramidkv_update: copy frame (src_frame, src_head) of new_k/new_v
  * [F,H,FSEQ,D] (and new_pos [F,H,FSEQ,3] when non-NULL) into pool slot
- * dst_slot_global of pool dst_kind (0 sink / 1 middle / 2 recent; <0 skip). */
+ * dst_slot_global of pool dst_kind (0 sink / 1 middle / 2 recent).  Any
+ * other kind (SKIP -1; MERGE 5, which the reference's caller masks to -1
+ * first, _mega_cache.py:358-362, while its kernel would route it to the
+ * recent pool) writes nothing, and so do slots outside the pool and sources
+ * outside [frames_in_block, H]. */
 int pkv_update_frames(const pkv_geometry *geo, const pkv_pools *pools,
                       const uint16_t *new_k, const uint16_t *new_v,
                       const int64_t *new_pos, int32_t frames_in_block,
@@ -170,7 +174,11 @@ int pkv_merge_accum(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ,
  * device (held until the process ends); calls needing more
  * (pkv_merge_workspace_size(H, F, FSEQ, MTPA) above the limit: about H * F
  * <= 130 at FSEQ 1560) return PKV_ERR_CAPACITY.  Same kernels and results as
- * pkv_merge_accum.  Calls that overlap on one device race on the array. */
+ * pkv_merge_accum.  Calls that overlap on one device race on the array.
+ * The array's device address is looked up on the first call on each device
+ * and kept for the process; like every device pointer the process holds, it
+ * does not survive hipDeviceReset of that device (do not call this entry
+ * point after one). */
 #define PKV_MERGE_STATIC_SCRATCH_BYTES (1 << 20)
 
 int pkv_merge_accum_static(const uint8_t *states, int32_t H, int32_t F, int32_t FSEQ,

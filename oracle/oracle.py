@@ -284,15 +284,21 @@ def rope_apply(k_u16: np.ndarray, pos: np.ndarray, tables) -> np.ndarray:
 
 
 def update_frames(pools: dict, new_k, new_v, new_pos, H, FSEQ, D, kind, slot_global, src_frame, src_head):
-    """pyramidkv_update.cu:21-110 (pools mutated in place)."""
+    """pyramidkv_update.cu:21-110 (pools mutated in place): new_k/new_v
+    [F, H, FSEQ, D], new_pos [F, H, FSEQ, 3] or None; write i copies frame
+    (src_frame[i], src_head[i]) into slot slot_global[i] of pool kind[i]
+    (0 sink, 1 middle, 2 recent).  Other kinds, slots outside the pool and
+    sources outside [F, H] write nothing."""
     names = ["sink", "middle", "recent"]
     pk = (ctypes.c_void_p * 3)(*[_p(pools[n + "_k"]).value for n in names])
     pv = (ctypes.c_void_p * 3)(*[_p(pools[n + "_v"]).value for n in names])
     pp = (ctypes.c_void_p * 3)(*[_p(pools[n + "_pos"]).value for n in names])
+    nslots = np.array([pools[n + "_k"].size // (FSEQ * D) for n in names], np.int64)
+    F = new_k.size // (H * FSEQ * D)
     arrs = [np.ascontiguousarray(np.asarray(a, np.int32)) for a in (kind, slot_global, src_frame, src_head)]
-    lib().orc_update_frames(_p(new_k), _p(new_v), _p(new_pos) if new_pos is not None else None, ctypes.c_int(H),
-                            ctypes.c_int(FSEQ), ctypes.c_int(D), pk, pv, pp, *[_p(a) for a in arrs],
-                            ctypes.c_int(arrs[0].size))
+    lib().orc_update_frames(_p(new_k), _p(new_v), _p(new_pos) if new_pos is not None else None, ctypes.c_int(F),
+                            ctypes.c_int(H), ctypes.c_int(FSEQ), ctypes.c_int(D), pk, pv, pp, _p(nslots),
+                            *[_p(a) for a in arrs], ctypes.c_int(arrs[0].size))
 
 
 def merge_accum(states_layer, new_k, new_v, new_pos, desc, acc: dict, weights=None):

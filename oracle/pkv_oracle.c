@@ -415,14 +415,23 @@ void orc_rope_apply(const uint16_t *k, const int64_t *pos, int64_t n, int D, con
 
 /* ---------------- frame copy (pyramidkv_update.cu) ---------------- */
 
-void orc_update_frames(const uint16_t *new_k, const uint16_t *new_v, const int64_t *new_pos, int H, int FSEQ, int D,
-                       uint16_t *const *pk, uint16_t *const *pv, int64_t *const *ppos, const int32_t *kind,
-                       const int32_t *slot_global, const int32_t *src_frame, const int32_t *src_head, int n) {
+/* Kinds 0 / 1 / 2 name the sink / middle / recent pool; every other kind
+ * (SKIP -1, and MERGE 5, which the reference's caller masks to -1 before the
+ * op, _mega_cache.py:358-362) writes nothing, and so do slots outside the
+ * pool (nslots[kind]) and sources outside [F, H].  Within that domain this
+ * is the reference kernel's copy. */
+void orc_update_frames(const uint16_t *new_k, const uint16_t *new_v, const int64_t *new_pos, int F, int H, int FSEQ,
+                       int D, uint16_t *const *pk, uint16_t *const *pv, int64_t *const *ppos, const int64_t *nslots,
+                       const int32_t *kind, const int32_t *slot_global, const int32_t *src_frame,
+                       const int32_t *src_head, int n) {
   int op;
   for (op = 0; op < n; ++op) {
     const int k = kind[op];
     int64_t src, dstb;
-    if (k < 0) continue;
+    if (k < 0 || k > 2) continue;
+    if (slot_global[op] < 0 || slot_global[op] >= nslots[k] || src_frame[op] < 0 || src_frame[op] >= F ||
+        src_head[op] < 0 || src_head[op] >= H)
+      continue;
     src = ((int64_t)src_frame[op] * H + src_head[op]) * FSEQ * D;
     dstb = (int64_t)slot_global[op] * FSEQ * D;
     memcpy(pk[k] + dstb, new_k + src, (size_t)FSEQ * D * 2);

@@ -47,6 +47,51 @@ static void check_i32(const Tensor &t, const char *name) {
 
 constexpr int64_t kMaxMergeBlocks = 6, kMaxMergeActive = 2, kMaxMergeTokens = 420;
 
+// `t` is a contiguous tensor of `dtype` and exactly `shape` on `dev`.
+static void expect_tensor(const Tensor &t, at::ScalarType dtype, at::IntArrayRef shape, const c10::Device &dev,
+                          const char *op, const char *name) {
+  TORCH_CHECK(t.defined() && t.device() == dev, op, ": ", name, " must be on ", dev, " (got ",
+              t.defined() ? t.device().str() : std::string("undefined"), ")");
+  TORCH_CHECK(t.scalar_type() == dtype, op, ": ", name, " must be ", dtype, " (got ", t.scalar_type(), ")");
+  TORCH_CHECK(t.sizes() == shape, op, ": ", name, " must be ", shape, " (got ", t.sizes(), ")");
+  TORCH_CHECK(t.is_contiguous(), op, ": ", name, " must be contiguous");
+}
+
+// A descriptor array the kernels write: contiguous int32 on `dev` with at
+// least n entries.
+static void expect_desc(const Tensor &t, int64_t n, const c10::Device &dev, const char *op) {
+  TORCH_CHECK(t.device() == dev && t.scalar_type() == at::kInt && t.is_contiguous() && t.numel() >= n, op,
+              ": descriptor tensors must be contiguous int32 on ", dev, " with at least ", n, " entries (got ",
+              t.scalar_type(), " ", t.numel(), " on ", t.device(), ")");
+}
+
+// One layer's Veil merge tensors, with the extents every merge kernel
+// indexes: accumulators [H, MMA, MTPA, D] fp32, their positions
+// [H, MMA, MTPA, 3] int64, group ids [H, MMA, FSEQ] int32, tokens per group
+// [H, MMA, MTPA] fp32, group counts [H, MMA] int32 (weight sums [H, MMA] fp32
+// when given); the merge pools [H, MMB, MTPA, D] bf16, their positions
+// [H, MMB, MTPA, 3] int64 and token counts [H, MMB] int32.  MMA and MTPA are
+// read from acc_k, MMB from mk.
+static void expect_merge_layer(const char *op, const c10::Device &dev, int64_t H, int64_t FSEQ, int64_t D,
+                               const Tensor &acc_k, const Tensor &acc_v, const Tensor &acc_pos, const Tensor &acc_gid,
+                               const Tensor &acc_tpg, const Tensor &acc_ng, const Tensor *acc_wsum, const Tensor &mk,
+                               const Tensor &mv, const Tensor &mpos, const Tensor &mtc) {
+  TORCH_CHECK(acc_k.dim() == 4 && mk.dim() == 4, op, ": accum_sum_k must be [H, MMA, MTPA, D] and merge_k_pool "
+              "[H, MMB, MTPA, D]");
+  const int64_t MMA = acc_k.size(1), MTPA = acc_k.size(2), MMB = mk.size(1);
+  expect_tensor(acc_k, at::kFloat, {H, MMA, MTPA, D}, dev, op, "accum_sum_k");
+  expect_tensor(acc_v, at::kFloat, {H, MMA, MTPA, D}, dev, op, "accum_sum_v");
+  expect_tensor(acc_pos, at::kLong, {H, MMA, MTPA, 3}, dev, op, "accum_pos");
+  expect_tensor(acc_gid, at::kInt, {H, MMA, FSEQ}, dev, op, "accum_group_ids");
+  expect_tensor(acc_tpg, at::kFloat, {H, MMA, MTPA}, dev, op, "accum_tokens_per_group");
+  expect_tensor(acc_ng, at::kInt, {H, MMA}, dev, op, "accum_num_groups");
+  if (acc_wsum) expect_tensor(*acc_wsum, at::kFloat, {H, MMA}, dev, op, "accum_weight_sum");
+  expect_tensor(mk, at::kBFloat16, {H, MMB, MTPA, D}, dev, op, "merge_k_pool");
+  expect_tensor(mv, at::kBFloat16, {H, MMB, MTPA, D}, dev, op, "merge_v_pool");
+  expect_tensor(mpos, at::kLong, {H, MMB, MTPA, 3}, dev, op, "merge_pos_pool");
+  expect_tensor(mtc, at::kInt, {H, MMB}, dev, op, "merge_token_count");
+}
+
 // ---------------------------------------------------------------------------
 // PyramidKVCacheManager (pyramidkv_manager.h:62-199, .cc:36-214)
 // ---------------------------------------------------------------------------
@@ -379,9 +424,13 @@ static void mega_state_update(Tensor states, Tensor new_t_vals, Tensor d0, Tenso
   const int64_t need = num_heads * pkv_perhead_state_size();
   TORCH_CHECK(states.numel() >= need, "mega_state_update: states buffer too small (", states.numel(), " < ", need,
               ")");
-  TORCH_CHECK(new_t_vals.is_cuda() && new_t_vals.dtype() == at::kLong, "new_t_vals must be CUDA int64");
+  const c10::Device dev = states.device();
+  TORCH_CHECK(new_t_vals.device() == dev && new_t_vals.dtype() == at::kLong &&
+                  new_t_vals.numel() >= frames_in_block,
+              "new_t_vals must be int64 with frames_in_block entries on the states' device");
   for (const Tensor *t : {&d0, &d1, &d2, &d3, &d4, &d5, &d6, &d7}) {
     TORCH_CHECK(t->dtype() == at::kInt, "all descriptor tensors must be int32");
+    TORCH_CHECK(t->device() == dev, "descriptor tensors must be on the states' device ", dev);
     TORCH_CHECK(t->is_contiguous() && t->numel() >= num_heads * frames_in_block,
                 "descriptor tensors must be contiguous with num_heads * frames_in_block entries");
   }
@@ -475,16 +524,24 @@ static void merge_impl(Tensor states, Tensor new_k, Tensor new_v, Tensor new_pos
   TORCH_CHECK(new_pos.dim() == 4 && new_pos.size(0) == F && new_pos.size(1) == H && new_pos.size(2) == FSEQ &&
                   new_pos.size(3) == 3,
               "mega_merge_accum: new_pos must be [F,H,FSEQ,3]");
+  const c10::Device dev = new_k.device();
+  TORCH_CHECK(new_v.device() == dev && new_pos.device() == dev, "mega_merge_accum: new_k/v/pos on different devices");
+  expect_merge_layer("mega_merge_accum", dev, H, FSEQ, D, acc_k, acc_v, acc_pos, acc_gid, acc_tpg, acc_ng, wsum, mk,
+                     mv, mpos, mtc);
   const int64_t MMA = acc_k.size(1), MMB = mk.size(1), MTPA = acc_k.size(2);
-  for (const Tensor *t : {&acc_k, &acc_v, &acc_pos, &acc_gid, &acc_tpg, &acc_ng, &mk, &mv, &mpos, &mtc})
-    TORCH_CHECK(t->is_contiguous() && t->size(0) == H, "mega_merge_accum: accumulator / pool slices must be "
-                                                       "contiguous [H, ...] views of one layer");
-  TORCH_CHECK(states.dtype() == at::kByte && states.numel() >= H * pkv_perhead_state_size(),
-              "mega_merge_accum: states must hold H PerHeadState records");
+  TORCH_CHECK(states.device() == dev && states.dtype() == at::kByte &&
+                  states.numel() >= H * pkv_perhead_state_size(),
+              "mega_merge_accum: states must hold H PerHeadState records on the frames' device");
+  for (const Tensor *t : {&dk, &ds, &df, &dn}) {
+    TORCH_CHECK(t->device() == dev && t->scalar_type() == at::kInt && t->numel() >= H * F,
+                "mega_merge_accum: descriptor tensors must be int32 on ", dev, " with at least H * F = ", H * F,
+                " entries");
+  }
   if (H == 0 || F == 0) return;
   auto nk = new_k.contiguous(), nv = new_v.contiguous(), np = new_pos.contiguous();
   auto k0 = dk.contiguous(), k1 = ds.contiguous(), k2 = df.contiguous(), k3 = dn.contiguous();
   for (const Tensor *t : {&k0, &k1, &k2, &k3}) check_i32(*t, "merge descriptors");
+  TORCH_CHECK(!weights || weights->numel() == F, "mega_merge_accum_weighted: one weight per frame");
   Tensor st = states.contiguous();
   Tensor ws = at::empty({pkv_merge_workspace_size(H, F, FSEQ, MTPA)},
                         at::TensorOptions().dtype(at::kByte).device(nk.device()));
@@ -536,25 +593,18 @@ static void mega_evict_merge(Tensor states, Tensor new_t_vals, Tensor new_k, Ten
               "mega_evict_merge: new_k/new_v must be CUDA bf16 of equal shape");
   TORCH_CHECK(new_k.dim() == 4, "mega_evict_merge: new_k/new_v must be [F,H,FSEQ,D]");
   const int64_t F = new_k.size(0), H = new_k.size(1), FSEQ = new_k.size(2), D = new_k.size(3);
-  TORCH_CHECK(new_t_vals.is_cuda() && new_t_vals.dtype() == at::kLong && new_t_vals.numel() == F,
-              "mega_evict_merge: new_t_vals must be CUDA int64 [F]");
-  TORCH_CHECK(states.is_cuda() && states.dtype() == at::kByte && states.is_contiguous() &&
+  const c10::Device dev = new_k.device();
+  TORCH_CHECK(new_v.device() == dev, "mega_evict_merge: new_k/new_v on different devices");
+  TORCH_CHECK(new_t_vals.device() == dev && new_t_vals.dtype() == at::kLong && new_t_vals.numel() == F,
+              "mega_evict_merge: new_t_vals must be int64 [F] on the frames' device");
+  TORCH_CHECK(states.device() == dev && states.dtype() == at::kByte && states.is_contiguous() &&
                   states.numel() >= H * pkv_perhead_state_size(),
-              "mega_evict_merge: states must hold H PerHeadState records");
-  for (const Tensor *t : {&d0, &d1, &d2, &d3, &d4, &d5, &d6, &d7})
-    TORCH_CHECK(t->dtype() == at::kInt && t->is_contiguous() && t->numel() >= H * F,
-                "mega_evict_merge: descriptor tensors must be contiguous int32 with H * F entries");
-  TORCH_CHECK(acc_k.dtype() == at::kFloat && acc_v.dtype() == at::kFloat && acc_tpg.dtype() == at::kFloat &&
-                  acc_wsum.dtype() == at::kFloat,
-              "mega_evict_merge: accumulators must be fp32");
-  TORCH_CHECK(mk.dtype() == at::kBFloat16 && mv.dtype() == at::kBFloat16, "mega_evict_merge: merge pools must be bf16");
-  for (const Tensor *t : {&acc_k, &acc_v, &acc_pos, &acc_gid, &acc_tpg, &acc_ng, &acc_wsum, &mk, &mv, &mpos, &mtc})
-    TORCH_CHECK(t->is_cuda() && t->is_contiguous() && t->size(0) == H,
-                "mega_evict_merge: accumulator / pool slices must be contiguous [H, ...] CUDA views of one layer");
-  TORCH_CHECK(acc_k.dim() == 4 && acc_k.size(3) == D && acc_gid.dim() == 3 && acc_gid.size(2) == FSEQ,
-              "mega_evict_merge: accumulators must be [H, MMA, MTPA, D] with group ids [H, MMA, FSEQ]");
+              "mega_evict_merge: states must hold H PerHeadState records on the frames' device");
+  for (const Tensor *t : {&d0, &d1, &d2, &d3, &d4, &d5, &d6, &d7}) expect_desc(*t, H * F, dev, "mega_evict_merge");
+  expect_merge_layer("mega_evict_merge", dev, H, FSEQ, D, acc_k, acc_v, acc_pos, acc_gid, acc_tpg, acc_ng, &acc_wsum,
+                     mk, mv, mpos, mtc);
   const int64_t MMA = acc_k.size(1), MMB = mk.size(1), MTPA = acc_k.size(2);
-  TORCH_CHECK(workspace.is_cuda() && workspace.is_contiguous() &&
+  TORCH_CHECK(workspace.device() == dev && workspace.is_contiguous() &&
                   workspace.numel() * workspace.element_size() >= pkv_evict_merge_workspace_size(static_cast<int32_t>(H)),
               "mega_evict_merge: workspace must be a contiguous CUDA tensor of at least "
               "mega_evict_merge_workspace_size(num_heads) bytes, zero-filled before first use");
@@ -759,6 +809,11 @@ static void cache_update(Mgr mgr, Tensor states_layer, Tensor sink_caps_layer, T
               mgr->frame_seqlen(), ")");
   TORCH_CHECK(new_k.stride(3) == 1 && new_k.stride(2) == mgr->head_dim() && new_v.strides() == new_k.strides(),
               "cache_update: new_k/new_v must have dense [H, D] rows");
+  const c10::Device dev = mgr->valid_count().device();
+  TORCH_CHECK(new_k.device() == dev && new_v.device() == dev && states_layer.device() == dev &&
+                  sink_caps_layer.device() == dev && committed_vc_layer.device() == dev,
+              "cache_update: new_k/new_v, states_layer, sink_caps_layer and committed_vc_layer must be on the "
+              "manager's device ", dev);
   TORCH_CHECK(states_layer.dtype() == at::kByte && states_layer.is_contiguous() &&
                   states_layer.numel() >= mgr->num_heads() * pkv_perhead_state_size(),
               "cache_update: states_layer must be contiguous uint8 [H * 600]");

@@ -13,6 +13,11 @@ no snapshot copies).  A host-side marker per layer records the block whose
 shift is in the pool; an update for a different block while a noisy pass
 is uncommitted is rejected.
 
+The layers' Veil (merge) heads are read from the state records once, when
+``build_mega_caches`` builds the caches, and passed to every update as a
+bit mask: a record's strategy kind must not change afterwards (a record
+rewritten to Veil would advance its state machine without merging).
+
 ``attend`` builds the multi-chunk plan on the device, packs K/V (+3D RoPE)
 into the flat workspace and runs the ragged attention directly on q's
 [L_q, H, D] layout (no permutes).
@@ -64,7 +69,7 @@ class MegaCacheCtx:
     freqs: torch.Tensor = None
     freq_parts: tuple = None
     freq_parts_flat: tuple = None
-    # per layer: t0 of the block whose recent shift is in the pool but not committed
+    # per layer: (t0, frames) of the block whose recent shift is in the pool but not committed
     pending_block: list = field(default_factory=list)
     cu_q: dict = field(default_factory=dict)
 
@@ -102,11 +107,12 @@ class MegaCache:
         l = self.layer_idx
         if ctx.committed_vc is None:
             ctx.committed_vc = ctx.mgr.valid_count().clone()
+        block = (t0, L_in // FSEQ)
         pending = ctx.pending_block[l]
-        if pending is not None and pending != t0:
+        if pending is not None and pending != block:
             raise RuntimeError(
-                f"MegaCache.update: layer {l} has an uncommitted noisy pass for block t={pending}; "
-                f"commit it with a clean pass before updating block t={t0}")
+                f"MegaCache.update: layer {l} has an uncommitted noisy pass for block t={pending[0]} of "
+                f"{pending[1]} frames; commit it with a clean pass before updating block t={t0} of {block[1]} frames")
         clean = cache_update_mode == "clean"
         nk = new_k if new_k.dtype == torch.bfloat16 else new_k.to(torch.bfloat16)
         nv = new_v if new_v.dtype == torch.bfloat16 else new_v.to(torch.bfloat16)
@@ -116,9 +122,9 @@ class MegaCache:
             nv = nv.contiguous()
             nk = nk.contiguous()
         _ops.ops().cache_update(ctx.mgr, ctx.states_bytes[l], ctx.sink_caps_per_head[l], ctx.committed_vc[l], nk, nv,
-                                l, t0, 1 if clean else 0, 1 if pending == t0 else 0, ctx.spatial_width,
+                                l, t0, 1 if clean else 0, 1 if pending == block else 0, ctx.spatial_width,
                                 ctx.layer_merge_heads[l])
-        ctx.pending_block[l] = None if clean else t0
+        ctx.pending_block[l] = None if clean else block
 
     def last_update_descriptors(self, frames: int):
         """The 8 state-machine descriptor arrays of the last update call."""

@@ -1,62 +1,81 @@
-"""PyramidKVConfig: the per-(layer, head) metadata holder the reference's
-pipeline builds before choosing a cache (reference: pyramidkv/config.py:14-357;
-caller pipeline/causal_inference.py:707-762).
+"""PyramidKVConfig: the per-(layer, head) metadata the pipeline builds before
+it builds the cache (reference interface: pyramidkv/config.py:56-84; caller
+pipeline/causal_inference.py:707-762).
 
-It owns no device memory.  What it holds:
+The MegaCache branch of the caller reads one thing from it, ``capacity_map``,
+which it hands to ``factory.build_compositions`` before it builds the caches;
+``label_map``, ``code_map``, ``compositions`` (alias ``policies``) and the
+``get_layer_*`` views are kept for callers that inspect them.
 
-* ``capacity_map`` [L, H] int32 and ``label_map`` [L, H] int32, read from a
-  CSV that is either a label matrix (rows of more than three cells: each
-  cell a head label resolved to a capacity through ``code_map``; labels the
-  map lacks get ``default_capacity``) or explicit ``layer, head, capacity``
-  triples;
-* ``compositions`` (alias ``policies``): per-head HeadComposition lists
-  compiled by ``factory.build_compositions`` from the head-type CSV, or
-  None; the pipeline overwrites both with its own compile;
-* ``drop_head_mask`` / ``soft_ablate_head_mask`` [L, H] bool from
-  ``layer, head`` lists;
-* ``af_group_map``: the optional A-F head taxonomy, from a matrix CSV or
-  from a manifest / per-group directory of ``layer, head`` files.
+Head table format (the per-head classification CSV, e.g. the shipped
+``best_labels.csv``):
 
-The MegaCache path reads ``capacity_map`` and ``compositions``; the rest is
-carried for callers that read it.
+* a row of more than three cells is one layer of a label matrix; blank cells
+  are ignored, so row i gives the labels of heads 0, 1, ... of layer i;
+* a row of at most three cells is an explicit ``layer, head, capacity``
+  entry; rows that do not parse, or name a head outside the model, are
+  ignored;
+* when the file holds a label matrix, every head's capacity is
+  ``code_map[label]`` -- a label the map lacks (or a head the matrix does not
+  cover, whose label is "1") falls back to ``default_capacity`` when "1" is
+  not in the map either -- and ``label_map`` holds the label as an integer
+  (1 for labels that are not integers).
+
+``drop_heads_csv_path``, ``soft_ablate_heads_csv_path`` and the A-F
+taxonomy arguments are accepted, because the caller passes them, but their
+lists are not loaded: only the reference's per-chunk attention path
+(wan/modules/attention/core.py:260-266,323-350) applies them, and the
+MegaCache path does not.  Passing one of them warns once and leaves
+``drop_head_mask`` / ``soft_ablate_head_mask`` all False and ``af_group_map``
+all "".
 """
 from __future__ import annotations
 
 import csv
 import os
-from typing import Optional
+import warnings
+from typing import NamedTuple, Optional
 
+import numpy as np
 import torch
 
-_AF_GROUPS = ("A", "B", "C", "D", "E", "F")
-# consensus class ids of the taxonomy manifest -> group letter
-_AF_CLASS_IDS = {"A_RECENT_TRACKER": "A", "B_RHYTHM_DRIVER": "B", "C_WINDOW_SMOOTHER": "C",
-                 "D_CYCLE_ATTENDER": "D", "E_ANCHOR_SPARSE": "E", "F_BROAD_LOCAL": "F"}
-_announced: set = set()
+_DEFAULT_LABEL = "1"
+_warned: set = set()
 
 
-def _csv_rows(path: str):
+class HeadTable(NamedTuple):
+    """A parsed head CSV: the label-matrix rows (cells as strings, blanks
+    removed) and the explicit (layer, head, capacity) entries, in file
+    order."""
+    matrix: list
+    entries: list
+
+
+def read_head_table(path: str) -> HeadTable:
+    matrix, entries = [], []
     with open(path, newline="", encoding="utf-8") as f:
-        return [row for row in csv.reader(f) if row]
+        for cells in csv.reader(f):
+            if len(cells) > 3:
+                matrix.append([c.strip() for c in cells if c.strip()])
+                continue
+            try:
+                entries.append(tuple(int(c) for c in cells[:3]) if len(cells) == 3 else None)
+            except ValueError:
+                entries.append(None)
+    return HeadTable(matrix, [e for e in entries if e is not None])
 
 
-def _int_or_none(cell) -> int | None:
+def _label_value(label: str) -> int:
     try:
-        return int(str(cell).strip())
+        return int(label)
     except ValueError:
-        return None
+        return 1
 
 
-def _head_pairs(path: str, num_layers: int, num_heads: int):
-    """(layer, head) pairs of a CSV list; header and non-numeric rows skipped."""
-    pairs = []
-    for row in _csv_rows(path):
-        if len(row) < 2:
-            continue
-        l, h = _int_or_none(row[0]), _int_or_none(row[1])
-        if l is not None and h is not None and 0 <= l < num_layers and 0 <= h < num_heads:
-            pairs.append((l, h))
-    return pairs
+def _warn_once(key: str, message: str) -> None:
+    if key not in _warned:
+        _warned.add(key)
+        warnings.warn(message, stacklevel=3)
 
 
 class PyramidKVConfig:
@@ -69,8 +88,11 @@ class PyramidKVConfig:
         L, H = int(num_layers), int(num_heads)
         self.num_layers, self.num_heads = L, H
         self.frame_seq_length = frame_seq_length
+        self.default_capacity = int(default_capacity)
         if code_map is None:
-            code_map = {"-1": max(1, default_capacity // max(1, strategy_reduction_factor)), "1": default_capacity}
+            # oscillating heads (label -1) get a reduced window
+            code_map = {"-1": max(1, self.default_capacity // max(1, int(strategy_reduction_factor))),
+                        "1": self.default_capacity}
         self.code_map = {str(k): int(v) for k, v in code_map.items()}
         self.head_type_csv_path = head_type_csv_path
         self.drop_heads_csv_path = drop_heads_csv_path
@@ -78,143 +100,73 @@ class PyramidKVConfig:
         self.af_policy_enabled = bool(af_policy_enabled)
         self.af_csv_path, self.af_group_dir, self.af_manifest_path = af_csv_path, af_group_dir, af_manifest_path
 
-        self.capacity_map = torch.full((L, H), int(default_capacity), dtype=torch.int32)
-        self.label_map = torch.ones((L, H), dtype=torch.int32)
+        caps = np.full((L, H), self.default_capacity, np.int64)
+        labels = np.ones((L, H), np.int64)
+        if config_path and os.path.exists(config_path):
+            self._apply_head_table(read_head_table(config_path), caps, labels, config_path)
+        elif config_path:
+            _warn_once(f"missing:{config_path}", f"PyramidKVConfig: {config_path} does not exist; every head keeps "
+                                                 f"capacity {self.default_capacity}")
+        self.capacity_map = torch.from_numpy(caps.astype(np.int32))
+        self.label_map = torch.from_numpy(labels.astype(np.int32))
+
         self.drop_head_mask = torch.zeros((L, H), dtype=torch.bool)
         self.soft_ablate_head_mask = torch.zeros((L, H), dtype=torch.bool)
         self.af_group_map = [[""] * H for _ in range(L)]
+        for what, given in (("drop_heads_csv_path", drop_heads_csv_path),
+                            ("soft_ablate_heads_csv_path", soft_ablate_heads_csv_path),
+                            ("af_policy_enabled", self.af_policy_enabled)):
+            if given:
+                _warn_once(what, f"PyramidKVConfig: {what} is applied only by the per-chunk attention path, which "
+                                 f"this build does not include; the MegaCache path ignores it (masks stay empty)")
+        self._compositions = None
+        self._compiled = False
 
-        if config_path and os.path.exists(config_path):
-            if config_path not in _announced:
-                _announced.add(config_path)
-                print(f"PyramidKVConfig: capacities from {config_path}")
-            self._load_capacities(config_path, int(default_capacity))
-        elif config_path:
-            print(f"Warning: {config_path} does not exist; every head keeps capacity {default_capacity}.")
-
-        self.compositions = self._compile(head_type_csv_path)
-        self.policies = self.compositions
-
-        for path, mask, what in ((drop_heads_csv_path, self.drop_head_mask, "drop-head"),
-                                 (soft_ablate_heads_csv_path, self.soft_ablate_head_mask, "soft-ablate")):
-            if not path:
-                continue
-            if not os.path.exists(path):
-                print(f"Warning: {what} list {path} does not exist; none applied.")
-                continue
-            before = int(mask.sum())
-            for l, h in _head_pairs(path, L, H):
-                mask[l, h] = True
-            print(f"PyramidKVConfig: {what} list {path}: {int(mask.sum()) - before} heads")
-
-        if self.af_policy_enabled:
-            self._load_af_groups()
-
-    # -- capacities / labels ------------------------------------------------
-    def _load_capacities(self, path: str, default_capacity: int) -> None:
-        matrix = []
-        for row in _csv_rows(path):
-            if len(row) > 3:  # a label matrix row (one cell per head)
-                matrix.append([c.strip() for c in row if c.strip() != ""])
-                continue
-            if len(row) < 3:
-                continue
-            l, h, cap = (_int_or_none(c) for c in row[:3])
-            if None in (l, h, cap):
-                continue
-            if 0 <= l < self.num_layers and 0 <= h < self.num_heads:
-                self.capacity_map[l, h] = cap
-        if not matrix:
+    # -- head table -----------------------------------------------------------
+    def _apply_head_table(self, table: HeadTable, caps: np.ndarray, labels: np.ndarray, path: str) -> None:
+        L, H = caps.shape
+        for l, h, cap in table.entries:
+            if 0 <= l < L and 0 <= h < H:
+                caps[l, h] = cap
+        if not table.matrix:
             return
-        if len(matrix) != self.num_layers:
-            print(f"Warning: {path} has {len(matrix)} label rows for {self.num_layers} layers; "
-                  "missing layers keep the default capacity.")
-        unknown = set()
-        for l in range(self.num_layers):
-            cells = matrix[l] if l < len(matrix) else []
-            if cells and len(cells) != self.num_heads:
-                print(f"Warning: label row {l} has {len(cells)} cells for {self.num_heads} heads.")
-            for h in range(self.num_heads):
-                label = cells[h] if h < len(cells) else "1"
-                as_int = _int_or_none(label)
-                self.label_map[l, h] = 1 if as_int is None else as_int
-                if label in self.code_map:
-                    self.capacity_map[l, h] = self.code_map[label]
-                else:  # a class id is not a capacity
-                    self.capacity_map[l, h] = default_capacity
-                    unknown.add(label)
+        if len(table.matrix) != L or any(len(r) != H for r in table.matrix[:L]):
+            _warn_once(f"shape:{path}", f"PyramidKVConfig: {path} holds {len(table.matrix)} label rows of "
+                                        f"{sorted({len(r) for r in table.matrix})} cells for {L} layers x {H} "
+                                        f"heads; uncovered heads take label {_DEFAULT_LABEL}")
+        grid = np.full((L, H), _DEFAULT_LABEL, dtype=object)
+        for l, row in enumerate(table.matrix[:L]):
+            grid[l, :min(H, len(row))] = row[:H]
+        unknown = sorted({str(x) for x in grid.ravel()} - set(self.code_map))
+        caps[:] = np.vectorize(lambda s: self.code_map.get(s, self.default_capacity), otypes=[np.int64])(grid)
+        labels[:] = np.vectorize(_label_value, otypes=[np.int64])(grid)
         if unknown:
-            print(f"Warning: labels {sorted(unknown)} are not in code_map; those heads get capacity "
-                  f"{default_capacity}.")
+            _warn_once(f"labels:{path}", f"PyramidKVConfig: labels {unknown} of {path} are not in code_map; those "
+                                         f"heads get capacity {self.default_capacity}")
 
-    def _compile(self, head_type_csv_path):
-        path = head_type_csv_path
-        if not path:
-            fallback = os.path.join("configs", "head_configs", "best_labels.csv")
-            path = fallback if os.path.exists(fallback) else None
-        if not path or not os.path.exists(path):
-            return None
-        from .factory import build_compositions
-        try:
-            return build_compositions(num_layers=self.num_layers, num_heads=self.num_heads,
-                                      capacities=self.capacity_map, csv_path=path)
-        except Exception as e:  # the pipeline compiles its own compositions afterwards
-            print(f"Warning: head compositions from {path} failed: {e}")
-            return None
+    # -- compositions (compiled on first read; the pipeline assigns its own) --
+    @property
+    def compositions(self):
+        if not self._compiled:
+            self._compiled = True
+            path = self.head_type_csv_path
+            if path and os.path.exists(path):
+                from .factory import build_compositions
+                try:
+                    self._compositions = build_compositions(num_layers=self.num_layers, num_heads=self.num_heads,
+                                                            capacities=self.capacity_map, csv_path=path)
+                except Exception as e:  # the pipeline compiles its own from the same file next
+                    _warn_once(f"compile:{path}", f"PyramidKVConfig: head compositions from {path}: {e}")
+        return self._compositions
 
-    # -- A-F taxonomy -----------------------------------------------------------
-    def _set_group(self, l: int, h: int, group: str) -> bool:
-        if 0 <= l < self.num_layers and 0 <= h < self.num_heads and group in _AF_GROUPS:
-            changed = self.af_group_map[l][h] != group
-            self.af_group_map[l][h] = group
-            return changed
-        return False
+    @compositions.setter
+    def compositions(self, value):
+        self._compiled = True
+        self._compositions = value
 
-    def _load_af_groups(self) -> None:
-        counts = dict.fromkeys(_AF_GROUPS, 0)
-        if self.af_csv_path and os.path.exists(self.af_csv_path):
-            source = self.af_csv_path
-            with open(self.af_csv_path, newline="", encoding="utf-8") as f:
-                for l, row in enumerate(csv.reader(f)):
-                    for h, cell in enumerate(row[:self.num_heads]):
-                        g = str(cell).strip().upper()
-                        if self._set_group(l, h, g):
-                            counts[g] += 1
-        else:
-            group_dir, manifest = self.af_group_dir, self.af_manifest_path
-            if not group_dir and manifest:
-                group_dir = os.path.dirname(manifest)
-            if not manifest and group_dir and os.path.exists(os.path.join(group_dir, "taxonomy_heads_manifest.csv")):
-                manifest = os.path.join(group_dir, "taxonomy_heads_manifest.csv")
-            files = []
-            if manifest and os.path.exists(manifest):
-                with open(manifest, newline="", encoding="utf-8") as f:
-                    for row in csv.DictReader(f):
-                        cid, name = str(row.get("consensus_class_id", "")).strip(), str(row.get("file_name", "")).strip()
-                        if cid and name:
-                            files.append((cid, name))
-            elif group_dir and os.path.isdir(group_dir):
-                files = [(n[:-len("_heads.csv")], n) for n in os.listdir(group_dir) if n.endswith("_heads.csv")]
-            else:
-                print(f"Warning: A-F policy enabled without a taxonomy source (dir={group_dir}, manifest={manifest}).")
-            source = manifest or group_dir
-            for cid, name in files:
-                g = _AF_CLASS_IDS.get(cid)
-                path = name if os.path.isabs(name) else os.path.join(group_dir or "", name)
-                if not g or not os.path.exists(path):
-                    continue
-                with open(path, newline="", encoding="utf-8") as f:
-                    for row in csv.DictReader(f):
-                        l, h = _int_or_none(row.get("layer", "")), _int_or_none(row.get("head", ""))
-                        if l is not None and h is not None and self._set_group(l, h, g):
-                            counts[g] += 1
-        total = sum(counts.values())
-        if total:
-            print(f"PyramidKVConfig: A-F groups from {source}: " + ", ".join(f"{g}={counts[g]}" for g in _AF_GROUPS))
-        else:
-            print(f"Warning: A-F policy enabled but {source} assigned no heads.")
+    policies = compositions
 
-    # -- per-layer views --------------------------------------------------------
+    # -- per-layer views ----------------------------------------------------------
     def get_layer_capacities(self, layer_idx: int) -> list[int]:
         return self.capacity_map[layer_idx].tolist()
 

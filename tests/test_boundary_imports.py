@@ -4,10 +4,12 @@
   wan/modules/causal_model.py:2-3 and inference.py:191-192 are restated
   here as strings and executed against this package (the reference itself
   is never imported).
-* PyramidKVConfig (pyramidkv/config.py:14-357): the known answers of the
-  reference's tests/test_pyramidkv_config_robustness.py:15-59 and
-  tests/test_pyramidkv_config_af.py:20-100, plus the pipeline's flow
-  (causal_inference.py:707-762: config.capacity_map into build_compositions).
+* PyramidKVConfig (interface pyramidkv/config.py:56-84): the capacity /
+  label known answers of the reference's
+  tests/test_pyramidkv_config_robustness.py:15-59, the head-table format
+  rules, the out-of-scope head lists (accepted, not loaded) and the
+  pipeline's flow (causal_inference.py:707-762: config.capacity_map into
+  build_compositions).
 * PyramidKVCache / AdaptiveKVCache resolve for imports and isinstance and
   refuse construction with an error naming the MegaCache path.
 * The manager's strategy table (pyramidkv_manager.cc:160-214): the known
@@ -110,42 +112,62 @@ def test_config_defaults_and_reduction_factor(tmp_path):
     assert missing.get_layer_drop_mask(1) == [False] * 3 and missing.get_layer_af_groups(0) == [""] * 3
 
 
-@pytest.mark.parametrize("rows,L,H,want", [
-    ([["a", "b", "c"], ["d", "e", "f"]], 2, 3, [["A", "B", "C"], ["D", "E", "F"]]),
-    ([["A", "b", "C"]], 1, 3, [["A", "B", "C"]]),
-    ([["a", "x", "b"]], 1, 3, [["A", "", "B"]]),
-    ([["a", "b", "c", "d", "e"]], 1, 3, [["A", "B", "C"]]),
-    ([["a", "b"]], 3, 2, [["A", "B"], ["", ""], ["", ""]]),
-])
-def test_config_af_matrix_csv(tmp_path, rows, L, H, want):
+def test_config_head_table_format(tmp_path):
+    """Rows of more than three cells are label-matrix rows (blank cells
+    dropped); shorter rows are layer, head, capacity entries, applied before
+    the matrix resolves every head; entries outside the model or that do not
+    parse are ignored; non-integer labels read as 1 in label_map."""
     from pyramidkv import PyramidKVConfig
-    p = _write(tmp_path / "af.csv", rows)
-    manifest = _write(tmp_path / "manifest.csv", [["consensus_class_id", "file_name"]])
-    cfg = PyramidKVConfig(config_path=None, num_layers=L, num_heads=H, af_policy_enabled=True, af_csv_path=p,
-                          af_manifest_path=manifest)
-    assert cfg.af_group_map == want
-    off = PyramidKVConfig(config_path=None, num_layers=L, num_heads=H, af_policy_enabled=False, af_csv_path=p)
-    assert off.af_group_map == [[""] * H for _ in range(L)]
+    p = _write(tmp_path / "mixed.csv", [["layer", "head", "capacity"], ["0", "1", "7"], ["9", "0", "5"],
+                                        ["-1", "", "1", "osc", "2"], ["x", "1"], ["2", "-1", "1", "1"]])
+    cfg = PyramidKVConfig(config_path=p, num_layers=3, num_heads=4, default_capacity=90,
+                          code_map={"-1": 30, "1": 90, "2": 60})
+    assert cfg.get_layer_labels(0) == [-1, 1, 1, 2]  # "osc" is not an integer
+    assert cfg.get_layer_capacities(0) == [30, 90, 90, 60]  # the matrix overrides the entry (0, 1) -> 7
+    assert cfg.get_layer_capacities(1) == [60, 30, 90, 90]
+    assert cfg.get_layer_labels(2) == [1, 1, 1, 1] and cfg.get_layer_capacities(2) == [90] * 4  # uncovered layer
+    only = _write(tmp_path / "entries.csv", [["1", "1", "5"], ["0", "3", "8"], ["bad", "0", "1"], ["1", "0"]])
+    cfg = PyramidKVConfig(config_path=only, num_layers=2, num_heads=2, default_capacity=11)
+    assert cfg.capacity_map.tolist() == [[11, 11], [11, 5]] and cfg.label_map.tolist() == [[1, 1], [1, 1]]
+    no_one = _write(tmp_path / "no_one.csv", [["2", "-1", "2", "2"]])
+    cfg = PyramidKVConfig(config_path=no_one, num_layers=2, num_heads=4, default_capacity=50, code_map={"-1": 5})
+    assert cfg.capacity_map.tolist() == [[50, 5, 50, 50], [50, 50, 50, 50]]
 
 
-def test_config_af_manifest_and_head_lists(tmp_path):
+def test_config_compositions_compiled_on_first_read(tmp_path, monkeypatch):
+    from pyramidkv import PyramidKVConfig, factory
+    cfg = PyramidKVConfig(None, num_layers=30, num_heads=12, head_type_csv_path=factory.SHIPPED_LABELS_CSV)
+    assert cfg._compositions is None  # nothing compiled until read
+    comps = cfg.compositions
+    assert len(comps) == 30 and cfg.policies is comps
+    assert PyramidKVConfig(None, num_layers=2, num_heads=2).compositions is None
+    def refuse(**kw):
+        raise ValueError("unreadable head table")
+    monkeypatch.setattr(factory, "build_compositions", refuse)
+    bad = _write(tmp_path / "bad.csv", [["1", "1"], ["1", "1"]])
+    with pytest.warns(UserWarning, match="head compositions.*unreadable"):
+        assert PyramidKVConfig(None, num_layers=2, num_heads=2, head_type_csv_path=bad).compositions is None
+
+
+def test_config_out_of_scope_head_lists_are_not_loaded(tmp_path):
+    """The drop-head, soft-ablate and A-F lists are applied only by the
+    reference's per-chunk attention path (wan/modules/attention/core.py:
+    260-266,323-350), not by the MegaCache path: they are accepted, warn,
+    and leave the masks empty."""
     from pyramidkv import PyramidKVConfig
-    _write(tmp_path / "e_heads.csv", [["layer", "head"], ["0", "1"], ["1", "0"], ["9", "0"]])
-    _write(tmp_path / "b_heads.csv", [["layer", "head"], ["1", "1"]])
-    manifest = _write(tmp_path / "taxonomy_heads_manifest.csv",
-                      [["consensus_class_id", "file_name"], ["E_ANCHOR_SPARSE", "e_heads.csv"],
-                       ["B_RHYTHM_DRIVER", "b_heads.csv"], ["Z_UNKNOWN", "e_heads.csv"]])
-    cfg = PyramidKVConfig(config_path=None, num_layers=2, num_heads=2, af_policy_enabled=True,
-                          af_group_dir=str(tmp_path))
-    assert cfg.af_group_map == [["", "E"], ["E", "B"]]
-    assert PyramidKVConfig(config_path=None, num_layers=2, num_heads=2, af_policy_enabled=True,
-                           af_manifest_path=manifest).af_group_map == [["", "E"], ["E", "B"]]
-    drop = _write(tmp_path / "drop.csv", [["layer", "head"], ["0", "1"], ["5", "5"], ["x", "1"]])
-    soft = _write(tmp_path / "soft.csv", [["1", "0"]])
-    cfg = PyramidKVConfig(config_path=None, num_layers=2, num_heads=2, drop_heads_csv_path=drop,
-                          soft_ablate_heads_csv_path=soft)
-    assert cfg.drop_head_mask.tolist() == [[False, True], [False, False]]
-    assert cfg.get_layer_soft_ablate_mask(1) == [True, False]
+    from pyramidkv import config as C
+    drop = _write(tmp_path / "drop.csv", [["layer", "head"], ["0", "1"]])
+    af = _write(tmp_path / "af.csv", [["a", "b"], ["c", "d"]])
+    C._warned.clear()
+    with pytest.warns(UserWarning, match="ignores it") as rec:
+        cfg = PyramidKVConfig(config_path=None, num_layers=2, num_heads=2, drop_heads_csv_path=drop,
+                              soft_ablate_heads_csv_path=drop, af_policy_enabled=True, af_csv_path=af)
+    assert {str(w.message).split(":")[1].split()[0] for w in rec} == {"drop_heads_csv_path",
+                                                                      "soft_ablate_heads_csv_path",
+                                                                      "af_policy_enabled"}
+    assert not cfg.drop_head_mask.any() and not cfg.soft_ablate_head_mask.any()
+    assert cfg.af_group_map == [["", ""], ["", ""]] and cfg.get_layer_af_groups(1) == ["", ""]
+    assert cfg.drop_heads_csv_path == drop and cfg.af_policy_enabled and cfg.af_csv_path == af
 
 
 def test_config_to_compositions_pipeline_flow():

@@ -207,6 +207,13 @@ def test_update_frames_bit_exact():
         if (kind[i], sgl[i]) in seen:
             kind[i] = -1
         seen.add((kind[i], sgl[i]))
+    # entries that write nothing: MERGE (5; the reference's caller masks it to
+    # -1 before this op), a slot past the sink pool, a negative slot, a frame
+    # and a head outside the source
+    extra = np.array([[5, 0, 0, 0], [0, g.num_layers * H * g.max_sink, 1, 1], [2, -1, 0, 0], [1, 0, F, 0],
+                      [1, 1, 0, H]], np.int32)
+    kind, sgl, fr, hd = (np.concatenate([a, extra[:, j]]).astype(np.int32) for j, a in enumerate((kind, sgl, fr, hd)))
+    n = kind.size
     host = {k: dp.np(k).copy() for k in ["sink_k", "sink_v", "sink_pos", "middle_k", "middle_v", "middle_pos",
                                           "recent_k", "recent_v", "recent_pos"]}
     O.update_frames(host, nk, nv, npos, H, FS, D, kind, sgl, fr, hd)

@@ -212,3 +212,27 @@ def test_meta_dispatch_shapes():
     assert out.device.type == "meta" and tuple(out.shape) == (192, 4, 128)
     kr = torch.ops.adahead.rope_apply(k, torch.empty(1000, 3, dtype=torch.long, device="meta"), k, k, k)
     assert tuple(kr.shape) == (1000, 128)
+
+
+def test_megacache_rejects_a_second_block_while_a_noisy_pass_is_pending():
+    """The recent-window shift of a noisy pass stays in the pool until the
+    block's clean pass; an update for another block -- another t0, or the
+    same t0 with another frame count (whose shift differs) -- is refused
+    before anything is launched, and the pending marker is kept."""
+    from pyramidkv import _ops
+    if not _ops.available():
+        pytest.skip("torch binding not built")
+    from pyramidkv import factory
+    from pyramidkv._mega_cache import build_mega_caches
+    from pyramidkv.base import HeadComposition
+    H, D, FS = 2, 16, 8
+    comps = [[HeadComposition(f"h{h}", 0, sink_frames=1, recent_frames=3) for h in range(H)]]
+    cache = build_mega_caches(1, H, D, FS, 1, 1, 3, comps, max_attend_chunks=1, device="cpu", spatial_width=4,
+                              spatial_height=2, **factory.PYRAMID_FORCING_REMAP)[0]
+    kv = lambda F: torch.zeros(1, F * FS, H, D, dtype=torch.bfloat16)
+    cache.ctx.pending_block[0] = (5, 3)  # a noisy pass of block t=5 (3 frames) is in the pool
+    with pytest.raises(RuntimeError, match="uncommitted noisy pass for block t=5 of 3 frames"):
+        cache.update(kv(3), kv(3), 8 * FS, cache_update_mode="noisy")
+    with pytest.raises(RuntimeError, match="block t=5 of 2 frames"):
+        cache.update(kv(2), kv(2), 5 * FS, cache_update_mode="clean")
+    assert cache.ctx.pending_block[0] == (5, 3)

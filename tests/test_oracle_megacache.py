@@ -100,3 +100,57 @@ def test_positions_are_frame_and_grid_coordinates():
     tok = np.arange(6)
     assert ref.sink_pos[0, 0, 0].tolist() == [[5, t // 3, t % 3] for t in tok]
     assert ref.recent_pos[0, 0, 0].tolist() == [[6, t // 3, t % 3] for t in tok]
+
+
+def test_update_frames_closed_form_multi_head():
+    """orc_update_frames (pyramidkv_update.cu:21-110) against numpy indexing
+    of the [F, H, FSEQ, D] source and the [L, H, slots, FSEQ, D] pools: every
+    write lands new_k / new_v / new_pos[src_frame, src_head] in slot
+    slot_global of its pool; SKIP (-1), MERGE (5, which the reference's
+    caller masks before the op) and out-of-range writes leave every pool as
+    it was, and so do all slots no write names.  F != H, so a frame / head
+    swap in the source offset, or a pool mix-up, fails."""
+    rng = np.random.default_rng(11)
+    L, H, F, FS, D = 2, 3, 4, 24, 32
+    slots = dict(sink=2, middle=5, recent=3)
+    pools = {}
+    for n, s in slots.items():
+        pools[n + "_k"] = rng.integers(0, 1 << 16, (L, H, s, FS, D)).astype(np.uint16)
+        pools[n + "_v"] = rng.integers(0, 1 << 16, (L, H, s, FS, D)).astype(np.uint16)
+        pools[n + "_pos"] = rng.integers(-9, 9, (L, H, s, FS, 3)).astype(np.int64)
+    before = {k: v.copy() for k, v in pools.items()}
+    nk = rng.integers(0, 1 << 16, (F, H, FS, D)).astype(np.uint16)
+    nv = rng.integers(0, 1 << 16, (F, H, FS, D)).astype(np.uint16)
+    npos = rng.integers(100, 200, (F, H, FS, 3)).astype(np.int64)
+    names = ["sink", "middle", "recent"]
+    # distinct in-range destinations for kinds 0-2, plus SKIP / MERGE / out-of-range entries
+    writes, used = [], set()
+    while len(writes) < 14:
+        k = int(rng.integers(0, 3))
+        sg = int(rng.integers(0, L * H * slots[names[k]]))
+        if (k, sg) not in used:
+            used.add((k, sg))
+            writes.append((k, sg, int(rng.integers(0, F)), int(rng.integers(0, H))))
+    noop = [(-1, 0, 0, 0), (5, 1, 1, 1), (5, 0, 3, 2), (0, L * H * slots["sink"], 0, 0), (2, -1, 0, 0),
+            (1, 0, F, 0), (1, 1, 0, H)]
+    allw = writes + noop
+    order = rng.permutation(len(allw))
+    kind, sg, fr, hd = (np.array([allw[i][j] for i in order], np.int32) for j in range(4))
+    O.update_frames(pools, nk, nv, npos, H, FS, D, kind, sg, fr, hd)
+    want = {k: v.copy() for k, v in before.items()}
+    for k, s, f, h in writes:
+        n = names[k]
+        l, hh, slot = np.unravel_index(s, (L, H, slots[n]))
+        want[n + "_k"][l, hh, slot] = nk[f, h]
+        want[n + "_v"][l, hh, slot] = nv[f, h]
+        want[n + "_pos"][l, hh, slot] = npos[f, h]
+    for name in pools:
+        assert np.array_equal(pools[name], want[name]), name
+    # the writes did land (the pools are not merely unchanged)
+    assert sum(int((pools[n] != before[n]).any(axis=(-2, -1)).sum()) for n in pools if n.endswith("_k")) == 14
+    # without positions only K and V move
+    p2 = {k: v.copy() for k, v in before.items()}
+    O.update_frames(p2, nk, nv, None, H, FS, D, kind, sg, fr, hd)
+    for n in names:
+        assert np.array_equal(p2[n + "_pos"], before[n + "_pos"])
+        assert np.array_equal(p2[n + "_k"], want[n + "_k"])
