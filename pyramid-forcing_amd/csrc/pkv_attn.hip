@@ -68,6 +68,9 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBK = 64;  // keys per LDS tile
 constexpr float kHeadroom = 64.0f;  // bound of log2(P) in the fast pass
+// attn_p3_kernel: a wave whose rows' first-tile maxima (log2 units) all lie
+// in [kNoShiftLo, kNoShiftHi] takes P = 2^S without subtracting them
+constexpr float kNoShiftLo = -40.0f, kNoShiftHi = 24.0f;
 constexpr int kSchedMax = 1024;  // sequences the XCD-balanced schedule handles
 
 struct AttnParams {
@@ -204,6 +207,20 @@ __device__ inline float bf16x8_sum(bf16x8 p, float x) {
   const float a = __builtin_amdgcn_fdot2_f32_bf16(p0, one, x, false);
   const float b = __builtin_amdgcn_fdot2_f32_bf16(p1, one, 0.0f, false);
   return __builtin_amdgcn_fdot2_f32_bf16(p3, one, __builtin_amdgcn_fdot2_f32_bf16(p2, one, a, false), false) + b;
+}
+
+// x + the sum of the 8 bf16 values of p in one chain of four dot products
+// (the running row sum itself is the accumulator: no partial sums to add)
+__device__ inline float bf16x8_acc(bf16x8 p, float x) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 one;
+  one[0] = static_cast<__bf16>(1.0f);
+  one[1] = one[0];
+  const bf16x2 p0 = {p[0], p[1]}, p1 = {p[2], p[3]}, p2 = {p[4], p[5]}, p3 = {p[6], p[7]};
+  x = __builtin_amdgcn_fdot2_f32_bf16(p0, one, x, false);
+  x = __builtin_amdgcn_fdot2_f32_bf16(p1, one, x, false);
+  x = __builtin_amdgcn_fdot2_f32_bf16(p2, one, x, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(p3, one, x, false);
 }
 
 __device__ inline float half_sum(float x) {
@@ -551,6 +568,8 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 template <int N>
 using ic = std::integral_constant<int, N>;
+template <bool B>
+using bc = std::integral_constant<bool, B>;
 
 // s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
 // lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
@@ -949,8 +968,21 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
 // 12 intervals after it was issued, and every copy is issued at least 14
 // intervals before the first read of its tile (group 1's V copy at global
 // 6t+5, V(t+3) first read at 6t+19) and after the reads of the tile its slot
-// held were consumed.  Softmax, the fast / slow pass split and
-// the operand arrangement are those of attn_fwd_kernel.
+// held were consumed.  The operand arrangement and the slow pass are those
+// of attn_fwd_kernel.
+//
+// Softmax in this kernel takes the fewest vector instructions in L0, where
+// the exponentials already fill the SIMD's vector unit: Q is scaled by
+// c = scale * log2(e) once when it is loaded (rounded to bf16), so the S
+// product yields log2-domain scores and no per-score multiply is left.  A
+// row's reference m (its first tile's maximum) is fixed, so P may carry any
+// per-row factor: a wave whose rows all have m in [kNoShiftLo, kNoShiftHi]
+// takes P = 2^S with no subtraction at all (a scalar branch skips it), any
+// other wave P = 2^(S - m).  Each keeps P below 2^kHeadroom unless a later
+// key scores that far above its reference (0 or m), which the row sum shows
+// once at the end (any such P makes the sum reach the bound); the row sum
+// is one chain of v_dot2c_f32_bf16 into the running sum.  Against per-score
+// FMA, per-tile sums and checks, config 2 ran 6% faster.
 constexpr int kP3Waves = 12;
 constexpr int kP3Threads = 64 * kP3Waves;
 constexpr int kP3Rows = 32 * kP3Waves;
@@ -1014,6 +1046,13 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   // which cannot see the copies, then has no load of its own pending in the
   // key loop, where a wait for one would also wait for every copy in flight
   wait_vm<0>();
+  // Q scaled by c = softmax scale * log2(e) once and rounded to bf16, so the
+  // S product gives log2-domain scores (the rounding moves a score by about
+  // 2^-9 of |c q . k| / sqrt(D), a tenth of P's own bf16 rounding)
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qr[s][j] = static_cast<__bf16>(static_cast<float>(qr[s][j]) * c);
   f32x16 o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -1120,15 +1159,30 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
     float mq[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) mq[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
-    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c;
+    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
   };
+  // slow pass: P = 2^(S - m), returns the lane's sum
   auto probs = [&](const f32x16 &s, float mr, bf16x8 (&pb)[2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj)
-        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -mr)));
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj] - mr));
     return bf16x8_sum(pb[0], 0.0f) + bf16x8_sum(pb[1], 0.0f);
+  };
+  // fast pass: P = 2^(S - m) (shift) or 2^S, added to the running sum;
+  // shift is uniform over the wave, so this is a scalar branch
+  auto probs_fast = [&](f32x16 &s, bf16x8 (&pb)[2], bool shift) {
+    if (shift) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] -= m;
+      asm volatile("" : "+v"(s));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj]));
+    l = bf16x8_acc(pb[1], bf16x8_acc(pb[0], l));
   };
   // end of an interval: this wave's copies older than its 4 newest are
   // complete, then the workgroup barrier
@@ -1162,6 +1216,13 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
       mask(s, 0);
       m = tile_max(s);  // finite: the first tile holds key 0
     }
+    // The reference m of a row is fixed, so P may carry any per-row factor:
+    // a wave whose rows all have m in [kNoShiftLo, kNoShiftHi] takes P = 2^S
+    // itself (no subtraction; keys whose 2^S underflows weigh below 2^-86
+    // of the row's first-tile maximum), every other wave P = 2^(S - m).
+    // Either way P < 2^kHeadroom unless a later key scores that far above
+    // the reference (0 or m), which the row sum shows at the end.
+    const bool shift = __builtin_amdgcn_ballot_w64(wave_rows && !(m >= kNoShiftLo && m <= kNoShiftHi)) != 0;
     // group g runs two intervals behind group g - 1
     for (int i = 0; i < grp; ++i) {
       step();
@@ -1173,9 +1234,7 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
       constexpr int TT = decltype(tt_c)::value;
       // L0: P(t)
       mask(s, t * kPK);
-      const float ps = probs(s, m, pb);
-      l += ps;
-      ovf |= !(ps < exp2f(kHeadroom));
+      probs_fast(s, pb, shift);
       // the row sums are taken here, not sunk to a later interval where P
       // would have to stay live
       asm volatile("" : "+v"(l));
@@ -1234,6 +1293,8 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
       step();
     }
     wait_vm<0>();  // no copy may land in LDS after the workgroup ends
+    // a P at or above 2^kHeadroom makes the lane's sum reach it
+    ovf = !(l < exp2f(kHeadroom));
     if (ovf) ovf_any = 1;
     __syncthreads();
     if (ovf_any) {
