@@ -654,6 +654,12 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
   // which cannot see the copies, then has no load of its own pending in the
   // key loop, where a wait for one would also wait for every copy in flight
   wait_vm<0>();
+  // Q scaled by c = softmax scale * log2(e) once (rounded to bf16): the S
+  // product yields log2-domain scores (as in attn_p3_kernel)
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qr[s][j] = static_cast<__bf16>(static_cast<float>(qr[s][j]) * c);
   f32x16 o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -765,16 +771,31 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
     float mq[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) mq[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
-    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c;
+    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
   };
-  // P = 2^(S*c - mr) as the two 16-key B operands; returns the lane's sum
+  // slow pass: P = 2^(S - mr) as the two 16-key B operands; returns the
+  // lane's sum
   auto probs = [&](const f32x16 &s, float mr, bf16x8 (&pb)[2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj)
-        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -mr)));
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj] - mr));
     return bf16x8_sum(pb[0], 0.0f) + bf16x8_sum(pb[1], 0.0f);
+  };
+  // fast pass: P = 2^(S - m) (shift) or 2^S, added to the running sum;
+  // shift is uniform over the wave (attn_p3_kernel's reference modes)
+  auto probs_fast = [&](f32x16 &s, bf16x8 (&pb)[2], bool shift) {
+    if (shift) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] -= m;
+      asm volatile("" : "+v"(s));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj]));
+    l = bf16x8_acc(pb[1], bf16x8_acc(pb[0], l));
   };
 
   __shared__ int ovf_any;
@@ -799,6 +820,7 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
       m = tile_max(sa);  // finite: the first tile holds key 0
       load_k(Kb);
     }
+    const bool shift = __builtin_amdgcn_ballot_w64(wave_rows && !(m >= kNoShiftLo && m <= kNoShiftHi)) != 0;
     dma_v(Vc, 2);
     wait_vm<4>();  // V0 complete
     pp_barrier();
@@ -814,9 +836,7 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
       // compiler's own interleaving: pinning one MFMA between every two
       // exponentials with scheduling-group barriers ran 0.8% slower)
       gemm0(snext);
-      const float ps = probs(scur, m, pb);
-      l += ps;
-      ovf |= !(ps < exp2f(kHeadroom));
+      probs_fast(scur, pb, shift);
       pp_barrier();
       // I1: V(t) to registers, copy of K(t+4); K(t+2) complete after the wait
       load_v(vslot(ic<TT>()));
@@ -867,6 +887,8 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
     }
     if (grp == 0) pp_barrier();
     wait_vm<0>();  // no copy may land in LDS after the workgroup ends
+    // a P at or above 2^kHeadroom makes the lane's sum reach it
+    ovf = !(l < exp2f(kHeadroom));
     if (ovf) ovf_any = 1;
     __syncthreads();
     if (ovf_any) {

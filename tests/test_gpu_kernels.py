@@ -431,8 +431,10 @@ def test_attention_large_launch_keys_outscoring_the_first_tile_vs_float64():
     _attn_check(q, k, v, cu_q, cu_k, 86, 12)
 
 
-def test_attention_large_launch_reference_modes_vs_float64():
-    """The 12-wave kernel fixes each row's reference at its first key tile.
+@pytest.mark.parametrize("B", [86, 20])
+def test_attention_reference_modes_vs_float64(B):
+    """Both head_dim-128 kernels (86 x 12 pairs: the 12-wave kernel; 20 x 12:
+    the 8-wave one) fix each row's reference at its first key tile.
     A wave whose rows' first-tile maxima (log2 units) all lie in [-40, 24]
     takes P = 2^S unshifted, any other wave P = 2^(S - m); either falls back
     to the moving-maximum pass when a later key outscores the reference by
@@ -442,7 +444,7 @@ def test_attention_large_launch_reference_modes_vs_float64():
     headroom) and on both sides within one wave; spiked later keys reach
     ~98 units in unshifted rows."""
     rng = np.random.default_rng(17)
-    q, k, v, cu_q, cu_k = _large_launch_case(rng, True)
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, True, B=B)
     alpha = np.array([1.0, 2.0, 4.0], np.float32)[np.arange(q.shape[0]) % 3]
     q[:] = O.f32_to_bf16(np.broadcast_to(alpha[:, None, None], q.shape).astype(np.float32))
     lk = np.diff(cu_k)
@@ -452,7 +454,7 @@ def test_attention_large_launch_reference_modes_vs_float64():
         k[cu_k[s_]:cu_k[s_] + n] = O.f32_to_bf16(np.full((n, 128), betas[s_ % len(betas)], np.float32))
         if s_ % 7 == 3 and lk[s_] > 40:
             k[cu_k[s_] + lk[s_] - 1] = O.f32_to_bf16(np.full(128, 1.5, np.float32))
-    _attn_check(q, k, v, cu_q, cu_k, 86, 12)
+    _attn_check(q, k, v, cu_q, cu_k, B, 12)
 
 
 def test_attention_rejects_causal_and_bad_head_dim():
