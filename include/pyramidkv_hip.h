@@ -333,6 +333,20 @@ typedef struct pkv_attn_args {
 
 int pkv_ragged_attn_fwd(const pkv_attn_args *args, pkv_stream_t stream);
 
+/* The same attention with a device workspace (replaces the same call,
+ * _mega_cache.py:540-559).  Launches of head_dim 128 with fewer than 1,024
+ * query tiles of 384 rows (and at most 1,024 sequences) -- one layer's heads
+ * per call, as MegaCache.attend makes them -- split each sequence's keys
+ * into chunks so that the (query tile, chunk) items fill every compute unit
+ * evenly, and merge a query tile's chunks in a second launch, in chunk order
+ * (deterministic).  Other launches, or a workspace smaller than
+ * pkv_ragged_attn_workspace_size(), run as pkv_ragged_attn_fwd.  The
+ * workspace needs no initialisation; calls sharing one must be ordered (one
+ * stream). */
+int64_t pkv_ragged_attn_workspace_size(void);
+int pkv_ragged_attn_fwd_ws(const pkv_attn_args *args, void *workspace, int64_t workspace_bytes,
+                           pkv_stream_t stream);
+
 /* ---- fused MegaCache.update -------------------------------------------- */
 
 /* Bytes of device workspace pkv_cache_update needs for F frames per block.

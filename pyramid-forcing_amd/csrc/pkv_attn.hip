@@ -80,6 +80,11 @@ struct AttnParams {
   int Hq, kv_per_head, q_tiles, n_wg;
   int64_t q_tok, q_head, kv_tok, kv_head, o_tok, o_head;
   float scale_log2;
+  // key-split launches (attn_p3_kernel<true> + attn_combine_kernel): the
+  // per-item partial results and item records in the caller's workspace
+  float *part;
+  int4 *rec;
+  int n_seq, n_cu;
 };
 
 // Consecutive workgroup ids are dispatched round-robin over the 8 XCDs;
@@ -170,6 +175,121 @@ __device__ bool balanced_item(const int32_t *cu_q, const int32_t *cu_k, int Hq, 
   seq_out = res[0];
   qt_out = res[1];
   return seq_out >= 0;
+}
+
+// One item of a key-split launch: query tile qt of sequence seq against key
+// tiles [t_lo, t_hi) (32 keys each) of its k chunks (chunk j); the items of
+// sequence seq are numbered base + j * nq + qt.
+struct SplitItem {
+  int seq, qt, j, k, nq, base, t_lo, t_hi;
+};
+
+constexpr int kSplitRows = 384;  // query rows per item (attn_p3_kernel's workgroup)
+constexpr int kSplitKeys = 32;   // keys per key tile (attn_p3_kernel's kPK)
+
+// Key-split plan, computed by every workgroup of the launch in its prologue
+// (the same on each, from cu_q / cu_k alone).  Sequence s has nq_s query tiles
+// of kSplitRows rows and nkt_s key tiles; its keys split into
+// k_s = ceil(nkt_s / C) chunks of equal length (+-1 tile).  The chunk length
+// C is chosen among ceil(nkt_max / k), k = 1 .. kSplitMaxChunks, as the one
+// with the least estimated time ceil(items / n_cu) * (C + kSplitItemTiles)
+// (rounds of items over the compute units, each item's fixed cost counted
+// as kSplitItemTiles key tiles; fewer items on ties) among those with at
+// most n_items items.  Items are ranked by chunk length (longest first, ties
+// by sequence index), and a sequence's items ordered (chunk, query tile):
+// the query tiles of one chunk are consecutive, so they run at the same time
+// on one XCD and read the same keys through its L2.  Returns false when item
+// c does not exist.  scratch: 6 * kSchedMax ints of LDS, 16-byte aligned;
+// every thread must call it.
+constexpr int kSplitMaxChunks = 8;
+constexpr int kSplitItemTiles = 8;
+__device__ bool split_item(const AttnParams &p, int n_items, int c, int *scratch, SplitItem &out) {
+  const int n_seq = p.n_seq;
+  int *nq = scratch, *nkt = scratch + kSchedMax, *cost = scratch + 2 * kSchedMax;
+  int *order = scratch + 3 * kSchedMax, *items = scratch + 4 * kSchedMax, *kk = scratch + 5 * kSchedMax;
+  __shared__ int acc[3];
+  __shared__ SplitItem res;
+  const int n4 = (n_seq + 3) & ~3;
+  if (threadIdx.x == 0) {
+    acc[0] = 1;  // largest nkt (at least 1)
+    acc[1] = 0;
+    res.seq = -1;
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < n4; s += blockDim.x) {
+    int q = 0, t = 0;
+    if (s < n_seq) {
+      const int b = s / p.Hq;
+      q = (p.cu_q[b + 1] - p.cu_q[b] + kSplitRows - 1) / kSplitRows;
+      const int kv = p.kv_per_head ? s : b;
+      t = (p.cu_k[kv + 1] - p.cu_k[kv] + kSplitKeys - 1) / kSplitKeys;
+      if (q > 0) atomicMax(&acc[0], t);
+    }
+    nq[s] = q;
+    nkt[s] = t;
+  }
+  __syncthreads();
+  // chunk length: the candidate of least estimated time
+  const int nkt_max = acc[0];
+  int C = nkt_max;
+  int64_t best = -1;
+  for (int k1 = 1; k1 <= kSplitMaxChunks; ++k1) {
+    const int cand = (nkt_max + k1 - 1) / k1;
+    if (k1 > 1 && cand == (nkt_max + k1 - 2) / (k1 - 1)) continue;  // same length as k1 - 1
+    if (threadIdx.x == 0) acc[1] = 0;
+    __syncthreads();
+    int part = 0;
+    for (int s = threadIdx.x; s < n_seq; s += blockDim.x) part += nq[s] * max(1, (nkt[s] + cand - 1) / cand);
+    if (part) atomicAdd(&acc[1], part);
+    __syncthreads();
+    const int n_it = acc[1];
+    __syncthreads();
+    if (n_it > n_items) break;  // more chunks only add items
+    const int64_t t = static_cast<int64_t>((n_it + p.n_cu - 1) / p.n_cu) * (cand + kSplitItemTiles);
+    if (best < 0 || t < best) {
+      best = t;
+      C = cand;
+    }
+  }
+  for (int s = threadIdx.x; s < n4; s += blockDim.x) {
+    int k = 1, cs = -1;
+    if (s < n_seq && nq[s] > 0) {
+      k = max(1, (nkt[s] + C - 1) / C);
+      cs = (nkt[s] + k - 1) / k + 1;  // +1: fixed cost per item
+    }
+    kk[s] = k;
+    cost[s] = cs;
+    items[s] = s < n_seq ? nq[s] * k : 0;
+  }
+  __syncthreads();
+  // rank = sequences before s in (cost desc, index asc) order
+  for (int s = threadIdx.x; s < n_seq; s += blockDim.x) {
+    const int cs = cost[s];
+    int r = 0;
+    for (int t = 0; t < n_seq; ++t) r += (cost[t] > cs) || (cost[t] == cs && t < s);
+    order[r] = s;
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < n_seq; r += blockDim.x) {
+    int base = 0;
+    for (int rr = 0; rr < r; ++rr) base += items[order[rr]];
+    const int s = order[r];
+    if (c >= base && c < base + items[s]) {
+      const int local = c - base, q = nq[s], k = kk[s];
+      res.seq = s;
+      res.j = local / q;
+      res.qt = local % q;
+      res.k = k;
+      res.nq = q;
+      res.base = base;
+      res.t_lo = static_cast<int>(static_cast<int64_t>(res.j) * nkt[s] / k);
+      res.t_hi = static_cast<int>(static_cast<int64_t>(res.j + 1) * nkt[s] / k);
+    }
+  }
+  __syncthreads();
+  out = res;
+  __syncthreads();  // the scratch is reused by the caller
+  return out.seq >= 0;
 }
 
 __device__ inline uint4 ldg16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -562,6 +682,7 @@ __global__ void __launch_bounds__(kThreads, 1) attn_fwd_kernel(AttnParams p) {
 constexpr int kPK = 32;                 // keys per tile
 constexpr int kPRow = 256;              // LDS bytes per key row (128 bf16)
 constexpr int kPTileElems = kPK * 128;  // bf16 elements per tile
+static_assert(kPK == kSplitKeys, "the key-split plan counts attn_p3_kernel's key tiles");
 
 typedef __attribute__((address_space(3))) char lds_char;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -1009,14 +1130,29 @@ constexpr int kP3Waves = 12;
 constexpr int kP3Threads = 64 * kP3Waves;
 constexpr int kP3Rows = 32 * kP3Waves;
 constexpr int kP3MinGrid = 1024;  // workgroups: four per CU
+// a key-split item's partial result: per wave its lanes' 64 O^T values
+// (16 float4 per lane, lane-minor) and then per wave and lane (r, l)
+constexpr int kPartOFloats = kP3Waves * 16 * 64 * 4;
+constexpr int kPartFloats = kPartOFloats + kP3Waves * 64 * 2;
 
+static_assert(kP3Rows == kSplitRows, "a key-split item is one attn_p3_kernel workgroup");
+
+// SPLIT: the workgroup runs item xcd_remap(blockIdx.x) of the key-split plan
+// (split_item): one query tile against one chunk of its sequence's keys.
+// An item whose sequence has one chunk writes O as the plain kernel does;
+// otherwise it writes its partial result (unnormalised O^T, the reference r
+// its probabilities were taken against -- 0, m, or the slow pass's final
+// maximum -- and the row sum l, per lane) to part slot c, and
+// attn_combine_kernel merges a query tile's chunks.  Every workgroup writes
+// its item's record (k = 0 when the item does not exist).
+template <bool SPLIT>
 __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   // the eight tile slots (K 0-3, V 4-7) in one 64 KB array at the start of
   // LDS, so that every fragment read addresses its slot by an immediate
   // offset; the work-list scratch of the prologue shares it (no copy is
   // issued before the work list is read)
   __shared__ __attribute__((aligned(16))) uint16_t kv[8 * kPTileElems];
-  static_assert(8 * kPTileElems * 2 >= 4 * kSchedMax * 4, "work-list scratch fits in the tile slots");
+  static_assert(8 * kPTileElems * 2 >= 6 * kSchedMax * 4, "work-list scratch fits in the tile slots");
   int *sched = reinterpret_cast<int *>(kv);
   auto kslot = [&](auto s) -> uint16_t * { return kv + (decltype(s)::value & 3) * kPTileElems; };
   auto vslot = [&](auto s) -> uint16_t * { return kv + (4 + (decltype(s)::value & 3)) * kPTileElems; };
@@ -1024,15 +1160,25 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   uint16_t *const Va = vslot(ic<0>()), *const Vb = vslot(ic<1>()), *const Vc = vslot(ic<2>());
 
   int seq, qt;
-  const int n_seq = p.n_wg / p.q_tiles;
-  if (n_seq <= kSchedMax) {
-    if (!balanced_item(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, kP3Rows, xcd_remap(blockIdx.x, p.n_wg), sched,
-                       seq, qt))
-      return;
+  SplitItem it{};
+  if constexpr (SPLIT) {
+    const int c = xcd_remap(blockIdx.x, p.n_wg);
+    const bool ok = split_item(p, p.n_wg, c, sched, it);
+    if (threadIdx.x == 0) p.rec[c] = ok ? make_int4(it.seq, it.qt, it.j | (it.k << 16), it.nq) : make_int4(0, 0, 0, 0);
+    if (!ok) return;
+    seq = it.seq;
+    qt = it.qt;
   } else {
-    const int wg = xcd_remap(blockIdx.x, p.n_wg);
-    seq = wg / p.q_tiles;
-    qt = wg % p.q_tiles;
+    const int n_seq = p.n_wg / p.q_tiles;
+    if (n_seq <= kSchedMax) {
+      if (!balanced_item(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, kP3Rows, xcd_remap(blockIdx.x, p.n_wg), sched,
+                         seq, qt))
+        return;
+    } else {
+      const int wg = xcd_remap(blockIdx.x, p.n_wg);
+      seq = wg / p.q_tiles;
+      qt = wg % p.q_tiles;
+    }
   }
   const int b = seq / p.Hq, h = seq % p.Hq;
   const int q_begin = p.cu_q[b];
@@ -1040,8 +1186,13 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   const int q0 = qt * kP3Rows;
   if (q0 >= Lq) return;
   const int kv_idx = p.kv_per_head ? seq : b;
-  const int k_begin = p.cu_k[kv_idx];
-  const int Lk = p.cu_k[kv_idx + 1] - k_begin;
+  int k_begin = p.cu_k[kv_idx];
+  int Lk = p.cu_k[kv_idx + 1] - k_begin;
+  if constexpr (SPLIT) {  // this item's chunk of the keys
+    const int lo = min(it.t_lo * kPK, Lk), hi = min(it.t_hi * kPK, Lk);
+    k_begin += lo;
+    Lk = hi - lo;
+  }
   const uint16_t *qp = p.q + static_cast<int64_t>(q_begin) * p.q_tok + h * p.q_head;
   const int64_t kv_off = static_cast<int64_t>(k_begin) * p.kv_tok + (p.kv_per_head ? 0 : h * p.kv_head);
   const uint16_t *kp = p.k + kv_off;
@@ -1081,6 +1232,7 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
   float m = -INFINITY, l = 0.0f;
+  float ref = 0.0f;  // the reference P was taken against (partial results of key-split items)
   const int nT = (Lk + kPK - 1) / kPK;
 
   // ---- tile copies (groups 0 and 1): buffer resources based at the tile's
@@ -1317,6 +1469,7 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
     wait_vm<0>();  // no copy may land in LDS after the workgroup ends
     // a P at or above 2^kHeadroom makes the lane's sum reach it
     ovf = !(l < exp2f(kHeadroom));
+    ref = shift ? m : 0.0f;
     if (ovf) ovf_any = 1;
     __syncthreads();
     if (ovf_any) {
@@ -1359,6 +1512,22 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
         }
         __syncthreads();
       }
+      ref = m;
+    }
+  }
+
+  if constexpr (SPLIT) {
+    if (it.k > 1) {
+      // partial result of this chunk, in the lane layout attn_combine_kernel reads
+      if (!wave_rows) return;
+      float *slot = p.part + static_cast<int64_t>(xcd_remap(blockIdx.x, p.n_wg)) * kPartFloats;
+      float4 *po = reinterpret_cast<float4 *>(slot) + wave * 16 * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        po[j * 64] = make_float4(o[j / 4][4 * (j % 4)], o[j / 4][4 * (j % 4) + 1], o[j / 4][4 * (j % 4) + 2],
+                                 o[j / 4][4 * (j % 4) + 3]);
+      reinterpret_cast<float2 *>(slot + kPartOFloats)[wave * 64 + lane] = make_float2(ref, l);
+      return;
     }
   }
 
@@ -1380,6 +1549,122 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
         *reinterpret_cast<bf16x4 *>(orow + d) = v;
       }
   }
+}
+
+// Second launch of a key-split attention: item c with chunk j = 0 of a
+// split query tile (k > 1 chunks) merges the partial results of items
+// c + j' * nq, j' = 0 .. k-1, in that order: with M the largest reference,
+// O = sum_j' 2^(r_j' - M) O_j' / sum_j' 2^(r_j' - M) l_j' (fp32), written
+// as attn_p3_kernel's epilogue writes it.  Other items exit at once.
+__global__ void __launch_bounds__(kP3Threads) attn_combine_kernel(AttnParams p) {
+  const int c = blockIdx.x;
+  const int4 r = p.rec[c];
+  const int k = r.z >> 16, j = r.z & 0xffff;
+  if (k <= 1 || j != 0) return;
+  const int seq = r.x, qt = r.y, nq = r.w;
+  const int b = seq / p.Hq, h = seq % p.Hq;
+  const int q_begin = p.cu_q[b];
+  const int Lq = p.cu_q[b + 1] - q_begin;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int q0 = qt * kP3Rows;
+  if (q0 + wave * 32 >= Lq) return;
+  auto slot = [&](int jj) { return p.part + static_cast<int64_t>(c + jj * nq) * kPartFloats; };
+  float M = -INFINITY;
+  for (int jj = 0; jj < k; ++jj) M = fmaxf(M, reinterpret_cast<const float2 *>(slot(jj) + kPartOFloats)[wave * 64 + lane].x);
+  float l = 0.0f;
+  float4 acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int jj = 0; jj < k; ++jj) {
+    const float *sp = slot(jj);
+    const float2 rl = reinterpret_cast<const float2 *>(sp + kPartOFloats)[wave * 64 + lane];
+    const float w = __builtin_amdgcn_exp2f(rl.x - M);
+    l = fmaf(w, rl.y, l);
+    const float4 *po = reinterpret_cast<const float4 *>(sp) + wave * 16 * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4 v = po[i * 64];
+      acc[i].x = fmaf(w, v.x, acc[i].x);
+      acc[i].y = fmaf(w, v.y, acc[i].y);
+      acc[i].z = fmaf(w, v.z, acc[i].z);
+      acc[i].w = fmaf(w, v.w, acc[i].w);
+    }
+  }
+  const float lt = half_sum(l);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  const int row_q = q0 + wave * 32 + lq;
+  if (row_q < Lq) {
+    uint16_t *orow = p.o + static_cast<int64_t>(q_begin + row_q) * p.o_tok + h * p.o_head;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
+        const float4 v = acc[4 * db + g];
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        bf16x4 o4;
+        o4[0] = static_cast<__bf16>(v.x * inv);
+        o4[1] = static_cast<__bf16>(v.y * inv);
+        o4[2] = static_cast<__bf16>(v.z * inv);
+        o4[3] = static_cast<__bf16>(v.w * inv);
+        *reinterpret_cast<bf16x4 *>(orow + d) = o4;
+      }
+  }
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Items a key-split launch may have: three per compute unit.
+static int64_t split_items() { return 3 * static_cast<int64_t>(device_cus()); }
+static int64_t split_ws_bytes(int64_t items) {
+  return items * (static_cast<int64_t>(kPartFloats) * 4 + static_cast<int64_t>(sizeof(int4)));
+}
+
+// Key-split launch (head_dim 128): attn_p3_kernel<true> over n items, then
+// attn_combine_kernel.  Returns -1 when the launch does not qualify (the
+// caller then runs the plain kernels).
+static int launch_split(const pkv_attn_args *a, void *ws, int64_t ws_bytes, hipStream_t st) {
+  const int64_t seqs = static_cast<int64_t>(a->num_batches) * a->num_heads_q;
+  const int64_t q_tiles = (a->max_seqlen_q + kP3Rows - 1) / kP3Rows;
+  const int64_t n = split_items();
+  // small launches only: those the 12-wave kernel would not fill the chip with
+  // per-head keys only (the cache's attention; a shared key sequence, as in
+  // cross-attention to a short text context, gains nothing from splitting)
+  if (!ws || a->head_dim != 128 || !a->kv_per_head || n <= 0 || seqs > kSchedMax ||
+      seqs * q_tiles >= kP3MinGrid || seqs * q_tiles > n || ws_bytes < split_ws_bytes(n))
+    return -1;
+  AttnParams p;
+  p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o;
+  p.cu_q = a->cu_seqlens_q; p.cu_k = a->cu_seqlens_k;
+  p.Hq = a->num_heads_q;
+  p.kv_per_head = a->kv_per_head;
+  p.q_tiles = static_cast<int>(q_tiles);
+  p.n_wg = static_cast<int>(n);
+  p.n_seq = static_cast<int>(seqs);
+  p.n_cu = device_cus();
+  p.q_tok = a->q_tok_stride; p.q_head = a->q_head_stride;
+  p.kv_tok = a->kv_tok_stride; p.kv_head = a->kv_head_stride;
+  p.o_tok = a->o_tok_stride; p.o_head = a->o_head_stride;
+  p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
+  p.part = static_cast<float *>(ws);
+  p.rec = reinterpret_cast<int4 *>(static_cast<char *>(ws) + n * static_cast<int64_t>(kPartFloats) * 4);
+  hipLaunchKernelGGL(attn_p3_kernel<true>, dim3(p.n_wg), dim3(kP3Threads), 0, st, p);
+  int rc = check_launch("attn_p3_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(p.n_wg), dim3(kP3Threads), 0, st, p);
+  return check_launch("attn_combine_kernel");
 }
 
 template <int D>
@@ -1405,7 +1690,7 @@ static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   if (p.n_wg == 0) return PKV_OK;
   if (p3) {
-    hipLaunchKernelGGL(attn_p3_kernel, dim3(p.n_wg), dim3(kP3Threads), 0, st, p);
+    hipLaunchKernelGGL(attn_p3_kernel<false>, dim3(p.n_wg), dim3(kP3Threads), 0, st, p);
     return check_launch("attn_p3_kernel");
   }
   if (D == 128) {
@@ -1419,6 +1704,38 @@ static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
 }  // namespace pkv
 
 using namespace pkv;
+
+// checks shared by both entry points; 1 = nothing to do
+static int attn_check(const pkv_attn_args *a) {
+  if (!a || !a->q || !a->k || !a->v || !a->o || !a->cu_seqlens_q || !a->cu_seqlens_k)
+    return fail(PKV_ERR_INVALID, "ragged_attn: NULL argument");
+  if (a->causal) return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: causal masking is not implemented (causal=False only)");
+  if (a->num_batches < 0 || a->num_heads_q <= 0 || a->max_seqlen_q < 0)
+    return fail(PKV_ERR_INVALID, "ragged_attn: bad sizes");
+  if (a->num_batches == 0 || a->max_seqlen_q == 0) return 1;
+  if ((a->q_tok_stride & 7) || (a->q_head_stride & 7) || (a->kv_tok_stride & 7) || (a->kv_head_stride & 7) ||
+      (a->o_tok_stride & 3) || (a->o_head_stride & 3))
+    return fail(PKV_ERR_INVALID, "ragged_attn: strides must keep 16-byte rows aligned");
+  if (a->kv_tok_stride * 2 * kBK > 0x7fffffff)
+    return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: kv token stride too large");
+  if (a->head_dim != 128 && a->head_dim != 64)
+    return fail(PKV_ERR_UNSUPPORTED, "ragged_attn: head_dim %d (supported: 64, 128)", a->head_dim);
+  return 0;
+}
+
+extern "C" int64_t pkv_ragged_attn_workspace_size(void) {
+  const int64_t n = split_items();
+  return n > 0 ? split_ws_bytes(n) : 0;
+}
+
+extern "C" int pkv_ragged_attn_fwd_ws(const pkv_attn_args *a, void *workspace, int64_t workspace_bytes,
+                                      pkv_stream_t stream) {
+  const int rc = attn_check(a);
+  if (rc) return rc < 0 ? rc : PKV_OK;
+  const int s = launch_split(a, workspace, workspace_bytes, as_stream(stream));
+  if (s >= 0) return s;
+  return pkv_ragged_attn_fwd(a, stream);
+}
 
 extern "C" int pkv_ragged_attn_fwd(const pkv_attn_args *a, pkv_stream_t stream) {
   if (!a || !a->q || !a->k || !a->v || !a->o || !a->cu_seqlens_q || !a->cu_seqlens_k)

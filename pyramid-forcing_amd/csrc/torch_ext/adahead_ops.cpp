@@ -648,7 +648,8 @@ static int64_t mega_evict_merge_workspace_size(int64_t num_heads) {
 // entries (sequence b*Hq+h); otherwise k/v are [total_k, Hq, D] with
 // cu_seqlens_k [num_batches+1].  Returns the output shaped like q.
 static Tensor ragged_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k,
-                               int64_t max_seqlen_q, double softmax_scale, bool kv_per_head, bool causal) {
+                               int64_t max_seqlen_q, double softmax_scale, bool kv_per_head, bool causal,
+                               c10::optional<Tensor> workspace) {
   TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "ragged_attention: tensors must be on the GPU");
   TORCH_CHECK(q.scalar_type() == at::kBFloat16 && k.scalar_type() == at::kBFloat16 &&
                   v.scalar_type() == at::kBFloat16,
@@ -695,9 +696,21 @@ static Tensor ragged_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q
   a.max_seqlen_q = static_cast<int32_t>(max_seqlen_q);
   a.softmax_scale = static_cast<float>(softmax_scale);
   a.causal = 0;
-  pkv_check(pkv_ragged_attn_fwd(&a, stream_for(q)), "ragged_attention");
+  if (workspace && workspace->defined() && workspace->numel() > 0) {
+    const Tensor &w = *workspace;
+    TORCH_CHECK(w.device() == q.device() && w.is_contiguous(),
+                "ragged_attention: workspace must be a contiguous tensor on q's device");
+    pkv_check(pkv_ragged_attn_fwd_ws(&a, w.data_ptr(), w.numel() * w.element_size(), stream_for(q)),
+              "ragged_attention");
+  } else {
+    pkv_check(pkv_ragged_attn_fwd(&a, stream_for(q)), "ragged_attention");
+  }
   return out;
 }
+
+// Bytes of the workspace ragged_attention splits small per-head-key launches
+// with (on the current device).
+static int64_t ragged_attention_workspace_size() { return pkv_ragged_attn_workspace_size(); }
 
 static Tensor rope_apply(Tensor k, Tensor pos, Tensor ft, Tensor fy, Tensor fx) {
   TORCH_CHECK(k.is_cuda() && k.scalar_type() == at::kBFloat16 && k.dim() == 2,
@@ -1101,7 +1114,7 @@ static adahead::Plan7 plan_multi(Mgr mgr, Tensor, int64_t, Tensor t_list, int64_
                                  int64_t, int64_t, int64_t, double) {
   return plan_shapes(mgr, t_list.numel());
 }
-static Tensor attn(Tensor q, Tensor, Tensor, Tensor, Tensor, int64_t, double, bool, bool) {
+static Tensor attn(Tensor q, Tensor, Tensor, Tensor, Tensor, int64_t, double, bool, bool, c10::optional<Tensor>) {
   return at::empty_like(q);
 }
 static Tensor rope(Tensor k, Tensor, Tensor, Tensor, Tensor) { return at::empty_like(k); }
@@ -1218,7 +1231,9 @@ TORCH_LIBRARY(adahead, m) {
         "Tensor(g!) accum_weight_sum, Tensor(h!) merge_k_pool, Tensor(i!) merge_v_pool, "
         "Tensor(j!) merge_pos_pool, Tensor(k!) merge_token_count) -> ()");
   m.def("ragged_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
-        "int max_seqlen_q, float softmax_scale, bool kv_per_head=True, bool causal=False) -> Tensor");
+        "int max_seqlen_q, float softmax_scale, bool kv_per_head=True, bool causal=False, "
+        "Tensor? workspace=None) -> Tensor");
+  m.def("ragged_attention_workspace_size() -> int");
   m.def("rope_apply(Tensor k, Tensor pos, Tensor freqs_ft_flat, Tensor freqs_fy_flat, Tensor freqs_fx_flat) "
         "-> Tensor");
   m.def("dit_layer_norm(Tensor x, Tensor? mul, Tensor? add, bool mul_plus_one, float eps) -> Tensor");
@@ -1273,6 +1288,7 @@ TORCH_LIBRARY_IMPL(adahead, CUDA, m) {
 TORCH_LIBRARY_IMPL(adahead, CompositeExplicitAutograd, m) {
   m.impl("mega_state_perhead_size", adahead::mega_state_perhead_size);
   m.impl("mega_evict_merge_workspace_size", adahead::mega_evict_merge_workspace_size);
+  m.impl("ragged_attention_workspace_size", adahead::ragged_attention_workspace_size);
   m.impl("mega_plan", adahead::mega_plan);
   m.impl("mega_plan_multi", adahead::mega_plan_multi);
   m.impl("update_descriptors", adahead::update_descriptors);

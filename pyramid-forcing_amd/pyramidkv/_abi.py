@@ -104,6 +104,9 @@ def lib():
                                       _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p]
         L.pkv_evict_merge_workspace_size.restype = _c_i64
         L.pkv_evict_merge_workspace_size.argtypes = [_c_i32]
+        L.pkv_ragged_attn_workspace_size.restype = _c_i64
+        L.pkv_ragged_attn_workspace_size.argtypes = []
+        L.pkv_ragged_attn_fwd_ws.argtypes = [_c_p, _c_p, _c_i64, _c_p]
         _lib = L
     return _lib
 
@@ -148,9 +151,15 @@ def rope_struct(tables):
                       fy.shape[1] // 2, fx.shape[0], fx.shape[1] // 2)
 
 
+def ragged_attn_workspace_size() -> int:
+    """Bytes of the workspace pkv_ragged_attn_fwd_ws splits small launches with."""
+    return int(lib().pkv_ragged_attn_workspace_size())
+
+
 def ragged_attn_fwd(q, k, v, out, cu_q, cu_k, num_batches, heads_q, kv_per_head, max_seqlen_q, scale,
-                    q_strides=None, kv_strides=None, o_strides=None):
-    """q/out [tokens, H, D] (or strided views), k/v [tokens, (H,) D]."""
+                    q_strides=None, kv_strides=None, o_strides=None, workspace=None):
+    """q/out [tokens, H, D] (or strided views), k/v [tokens, (H,) D]; with a
+    workspace tensor, pkv_ragged_attn_fwd_ws (key-split small launches)."""
     D = q.shape[-1]
     qs = q_strides or (q.stride(0), q.stride(1) if q.dim() == 3 else 0)
     ks = kv_strides or (k.stride(0), k.stride(1) if (k.dim() == 3 and k.shape[1] > 1) else 0)
@@ -158,4 +167,9 @@ def ragged_attn_fwd(q, k, v, out, cu_q, cu_k, num_batches, heads_q, kv_per_head,
     a = AttnArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), cu_q.data_ptr(), cu_k.data_ptr(),
                  num_batches, heads_q, D, 1 if kv_per_head else 0, qs[0], qs[1], ks[0], ks[1], os_[0], os_[1],
                  max_seqlen_q, float(scale), 0)
-    check(lib().pkv_ragged_attn_fwd(ctypes.byref(a), _c_p(stream_of(q))), "pkv_ragged_attn_fwd")
+    if workspace is not None:
+        check(lib().pkv_ragged_attn_fwd_ws(ctypes.byref(a), _c_p(workspace.data_ptr()),
+                                           ctypes.c_int64(workspace.numel() * workspace.element_size()),
+                                           _c_p(stream_of(q))), "pkv_ragged_attn_fwd_ws")
+    else:
+        check(lib().pkv_ragged_attn_fwd(ctypes.byref(a), _c_p(stream_of(q))), "pkv_ragged_attn_fwd")

@@ -72,6 +72,11 @@ class MegaCacheCtx:
     # per layer: (t0, frames) of the block whose recent shift is in the pool but not committed
     pending_block: list = field(default_factory=list)
     cu_q: dict = field(default_factory=dict)
+    # key-split attention for attend (off by default: on a rollout's per-layer
+    # launches it measured no faster than the unsplit kernels) and the
+    # device's workspace for it (_ops.attention_workspace)
+    split_attention: bool = False
+    attn_workspace: torch.Tensor = None
 
 
 class MegaCache:
@@ -200,8 +205,19 @@ class MegaCache:
             cu_q = ctx.cu_q[L_q] = torch.arange(0, L_q + 1, FSEQ, dtype=torch.int32, device=q.device)
         qb = q[0] if q.dtype == torch.bfloat16 else q[0].to(torch.bfloat16)
         out = _ops.ragged_attention(qb, ctx.mgr.k_flat_out().view(-1, D), ctx.mgr.v_flat_out().view(-1, D), cu_q,
-                                    cu_k, FSEQ, softmax_scale, kv_per_head=True, causal=causal)
+                                    cu_k, FSEQ, softmax_scale, kv_per_head=True, causal=causal,
+                                    workspace=self._split_workspace(q.device))
         return out.view(1, L_q, H, D).to(q.dtype)
+
+
+    def _split_workspace(self, device):
+        """The key-split attention workspace when ctx.split_attention is set."""
+        ctx = self.ctx
+        if not ctx.split_attention:
+            return None
+        if ctx.attn_workspace is None:
+            ctx.attn_workspace = _ops.attention_workspace(device)
+        return ctx.attn_workspace
 
 
 def _composition_to_perhead_state(composition: HeadComposition) -> ref.PerHeadState:

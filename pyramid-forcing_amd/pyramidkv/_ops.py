@@ -60,12 +60,33 @@ def pyramidkv_pack(mgr, src_kind, src_slot_global, seg_lengths, dst_token_offset
                          freqs_fx_flat if freqs_fx_flat is not None else ef)
 
 
+_attn_workspaces: dict = {}
+
+
+def attention_workspace(device) -> torch.Tensor:
+    """The device's workspace for ragged_attention's key-split launches
+    (allocated on first use and kept; it needs no initialisation).  Calls
+    sharing it must be ordered on one stream."""
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device(device.type, torch.cuda.current_device())
+    ws = _attn_workspaces.get(device)
+    if ws is None:
+        with torch.cuda.device(device):
+            n = int(ops().ragged_attention_workspace_size())
+        ws = _attn_workspaces[device] = torch.empty(max(n, 1), dtype=torch.uint8, device=device)
+    return ws
+
+
 def ragged_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_scale=None, kv_per_head=True,
-                     causal=False):
+                     causal=False, workspace=None):
+    """flash_attn_varlen_func's arithmetic (non-causal) on the ragged layout;
+    with a workspace (attention_workspace), launches of a few sequences with
+    per-head keys split their keys over every compute unit."""
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** -0.5
     return ops().ragged_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), float(softmax_scale),
-                                  bool(kv_per_head), bool(causal))
+                                  bool(kv_per_head), bool(causal), workspace)
 
 
 def scatter_copy(src_ptrs, lengths, offsets, dst, col_dim: int) -> None:

@@ -113,20 +113,24 @@ def _rand_bf16(rng, *shape):
 
 
 # (FS, W): 64 / 8 tiles into the Veil heads' 2 x 2 patches (member lists in
-# closed form); 63 / 9 does not (odd width: lists built from the group ids)
-@pytest.mark.parametrize("seed,block_sizes,noisy_passes,FS,W", [
-    (0, [3] * 9, 2, 64, 8),
-    (1, [1] + [3] * 8, 1, 64, 8),
-    (2, [2, 2, 3, 1, 3, 3, 2, 3, 4], 3, 64, 8),
-    (3, [3] * 6, 1, 63, 9),
-    (4, [2, 3, 1, 4, 3, 2], 2, 63, 9),
+# closed form); 63 / 9 does not (odd width: lists built from the group ids).
+# split: attend runs the key-split attention (ctx.split_attention).
+@pytest.mark.parametrize("seed,block_sizes,noisy_passes,FS,W,split", [
+    (0, [3] * 9, 2, 64, 8, False),
+    (1, [1] + [3] * 8, 1, 64, 8, False),
+    (2, [2, 2, 3, 1, 3, 3, 2, 3, 4], 3, 64, 8, False),
+    (3, [3] * 6, 1, 63, 9, False),
+    (4, [2, 3, 1, 4, 3, 2], 2, 63, 9, False),
+    (5, [3] * 9, 1, 64, 8, True),
 ])
-def test_megacache_rollout_bit_exact(seed, block_sizes, noisy_passes, FS, W):
+def test_megacache_rollout_bit_exact(seed, block_sizes, noisy_passes, FS, W, split):
     rng = np.random.default_rng(seed)
     L, H, D = 2, 6, 128
     labels = [[-1, 1, 2, -1, 1, 2], [2, -1, 1, 1, 2, -1]]
-    print(f"megacache rollout seed={seed} blocks={block_sizes} noisy={noisy_passes} FS={FS} W={W}", flush=True)
+    print(f"megacache rollout seed={seed} blocks={block_sizes} noisy={noisy_passes} FS={FS} W={W} split={split}",
+          flush=True)
     caches, ref, g = _build(L, H, D, FS, W, labels, chunks=4)
+    caches[0].ctx.split_attention = split
     t0 = 0
     for bi, F in enumerate(block_sizes):
         start = t0 * FS
