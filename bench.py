@@ -102,6 +102,66 @@ def bench_attention(steps: int, warmup: int, seed: int = 0):
                 q=q, k=k, v=v, out=out, cu_k=cu_k)
 
 
+def bench_attention_spiked(frac: float, units: float, steps: int, warmup: int, seed: int = 0):
+    """Config 2 with a fraction `frac` of every sequence's query rows given
+    one key, past the first key tile, aligned with the row's query so that
+    it scores `units` log2 units (scale * log2(e) * q.k) above zero, about
+    that far above the row's first-tile maximum; other rows see it near 0.
+    ~70 units: the fast pass rebases those rows after the tile; ~130: past
+    the rebase bound, their workgroups recompute in the slow pass.  Returns
+    the launch time (ms) and the worst error of one spiked sequence against
+    float64."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+    from pyramidkv import _abi as A
+
+    labels, lk = config2_lengths(seed)
+    r = bench_attention(1, 0, seed)
+    q, k, v, out, cu_k = r["q"], r["k"], r["v"], r["out"], r["cu_k"]
+    cu_q = torch.arange(0, L * QTOK + 1, QTOK, dtype=torch.int32, device=q.device)
+    c = (D ** -0.5) * 1.4426950408889634
+    rng = np.random.default_rng(seed + 7)
+    cuk = np.concatenate([[0], np.cumsum(lk.reshape(-1))])
+    n = max(1, int(round(frac * QTOK)))
+    rows_all, keys_all, heads_all = [], [], []
+    for s_ in range(L * H):
+        layer, head = divmod(s_, H)
+        rows = rng.choice(QTOK, size=n, replace=False) + layer * QTOK
+        keys = rng.choice(np.arange(32, int(lk.reshape(-1)[s_])), size=n, replace=False) + int(cuk[s_])
+        rows_all.append(rows)
+        keys_all.append(keys)
+        heads_all.append(np.full(n, head))
+    rows_t = torch.from_numpy(np.concatenate(rows_all)).to(q.device)
+    keys_t = torch.from_numpy(np.concatenate(keys_all)).to(q.device)
+    heads_t = torch.from_numpy(np.concatenate(heads_all)).to(q.device)
+    qv = q[rows_t, heads_t].float()
+    alpha = units / (c * (qv * qv).sum(-1, keepdim=True))
+    k[keys_t] = (alpha * qv).to(torch.bfloat16)
+
+    def step():
+        A.ragged_attn_fwd(q, k, v, out, cu_q, cu_k, L, H, True, QTOK, D ** -0.5)
+
+    for _ in range(max(1, warmup)):
+        step()
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(steps):
+        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_.record()
+        step()
+        e_.record()
+        torch.cuda.synchronize()
+        ms.append(s_.elapsed_time(e_))
+    # one spiked (layer 0, head 0) sequence against float64
+    f64 = lambda t: t.float().cpu().numpy().astype(np.float64)
+    want = O.attention_ref(f64(q[:QTOK, 0]), f64(k[:int(cuk[1])]), f64(v[:int(cuk[1])]), D ** -0.5)
+    err = np.abs(f64(out[:QTOK, 0]) - want)
+    return dict(ms=float(np.median(ms)), rows_per_sequence=n, units=units, max_abs=float(err.max()),
+                mean_abs=float(err.mean()), flops=r["flops"])
+
+
 def host_cpu() -> str:
     """Model name of the host CPU (first /proc/cpuinfo entry), for the CPU baselines."""
     try:
@@ -855,9 +915,27 @@ def config1_entry(args):
     return entry
 
 
+def spiked_entry(args):
+    """secondary.config2_spiked_rows: the headline launch with 1% / 10% of
+    the query rows each outscored by one key (fast-pass rebase at ~70 log2
+    units, slow pass at ~130)."""
+    import torch
+    out = {"definition": "config 2 with a fraction of each sequence's query rows given one key past the first tile "
+                         "scoring ~70 (rebased in the fast pass) or ~130 (slow pass) log2 units above the rest; "
+                         "attention ms per launch, error of one spiked sequence vs float64"}
+    for name, frac, units in (("rebase_1pct", 0.01, 70.0), ("rebase_10pct", 0.10, 70.0),
+                              ("slow_pass_1pct", 0.01, 130.0), ("slow_pass_10pct", 0.10, 130.0)):
+        r = bench_attention_spiked(frac, units, max(3, args.steps // 4), 1)
+        out[name] = {"ms": round(r["ms"], 4), "TFLOP/s": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
+                     "rows_per_sequence": r["rows_per_sequence"], "max_abs": round(r["max_abs"], 6),
+                     "mean_abs": round(r["mean_abs"], 7), "ok": bool(r["max_abs"] < 2e-2 and r["mean_abs"] < 2e-3)}
+        torch.cuda.empty_cache()
+    return out
+
+
 def secondary(args):
     import torch
-    out = {"config1_single_layer_step": config1_entry(args)}
+    out = {"config1_single_layer_step": config1_entry(args), "config2_spiked_rows": spiked_entry(args)}
     c3 = bench_cache_step(args.steps, args.warmup)
     ms = c3["graph_ms"] if c3["graph_ms"] is not None else c3["eager_ms"]
     gbs = c3["total_bytes"] / (ms * 1e-3) / 1e9

@@ -68,9 +68,10 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBK = 64;  // keys per LDS tile
 constexpr float kHeadroom = 64.0f;  // bound of log2(P) in the fast pass
-// attn_p3_kernel: a wave whose rows' first-tile maxima (log2 units) all lie
-// in [kNoShiftLo, kNoShiftHi] takes P = 2^S without subtracting them
-constexpr float kNoShiftLo = -40.0f, kNoShiftHi = 24.0f;
+// head_dim-128 kernels: a row sum in [2^kHeadroom, 2^kRebaseMax) after a
+// tile is rescaled in place; one at or above 2^kRebaseMax (or not finite)
+// sends the workgroup to the slow pass
+constexpr float kRebaseMax = 96.0f;
 constexpr int kSchedMax = 1024;  // sequences the XCD-balanced schedule handles
 
 struct AttnParams {
@@ -689,8 +690,6 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 template <int N>
 using ic = std::integral_constant<int, N>;
-template <bool B>
-using bc = std::integral_constant<bool, B>;
 
 // s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
 // lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
@@ -775,12 +774,6 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
   // which cannot see the copies, then has no load of its own pending in the
   // key loop, where a wait for one would also wait for every copy in flight
   wait_vm<0>();
-  // Q scaled by c = softmax scale * log2(e) once (rounded to bf16): the S
-  // product yields log2-domain scores (as in attn_p3_kernel)
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qr[s][j] = static_cast<__bf16>(static_cast<float>(qr[s][j]) * c);
   f32x16 o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -892,30 +885,26 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
     float mq[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) mq[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
-    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c;
   };
-  // slow pass: P = 2^(S - mr) as the two 16-key B operands; returns the
+  // slow pass: P = 2^(S*c - mr) as the two 16-key B operands; returns the
   // lane's sum
   auto probs = [&](const f32x16 &s, float mr, bf16x8 (&pb)[2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj)
-        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj] - mr));
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -mr)));
     return bf16x8_sum(pb[0], 0.0f) + bf16x8_sum(pb[1], 0.0f);
   };
-  // fast pass: P = 2^(S - m) (shift) or 2^S, added to the running sum;
-  // shift is uniform over the wave (attn_p3_kernel's reference modes)
-  auto probs_fast = [&](f32x16 &s, bf16x8 (&pb)[2], bool shift) {
-    if (shift) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] -= m;
-      asm volatile("" : "+v"(s));
-    }
+  // fast pass: P = 2^(S*c - m) against the row's reference m, added to the
+  // running sum (one chain of dot products)
+  auto probs_fast = [&](const f32x16 &s, bf16x8 (&pb)[2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj]));
+      for (int jj = 0; jj < 8; ++jj)
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -m)));
     l = bf16x8_acc(pb[1], bf16x8_acc(pb[0], l));
   };
 
@@ -941,7 +930,6 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
       m = tile_max(sa);  // finite: the first tile holds key 0
       load_k(Kb);
     }
-    const bool shift = __builtin_amdgcn_ballot_w64(wave_rows && !(m >= kNoShiftLo && m <= kNoShiftHi)) != 0;
     dma_v(Vc, 2);
     wait_vm<4>();  // V0 complete
     pp_barrier();
@@ -949,6 +937,26 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
     if (grp == 1) pp_barrier();
 
     bf16x8 pb[2];
+    // A row whose sum reached 2^kHeadroom met a key that far above its
+    // reference: after the tile's P*V product (I3) both lanes of the row scale O
+    // and their sums by the larger sum's power of two (exact) and raise the
+    // row's reference by as much.  A sum at or above 2^kRebaseMax, or not
+    // finite, leaves the workgroup to the slow pass.
+    auto rebase = [&]() {
+      const float lmax = half_max(l);
+      if (!(lmax < exp2f(kRebaseMax))) {
+        ovf = true;
+      } else if (!(lmax < exp2f(kHeadroom))) {
+        const int e = __builtin_amdgcn_frexp_expf(lmax);
+        const float f = __builtin_amdgcn_ldexpf(1.0f, -e);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= f;
+        l *= f;
+        m += static_cast<float>(e);
+      }
+    };
     auto iter = [&](auto tt_c, int t) {
       constexpr int TT = decltype(tt_c)::value;
       f32x16 &scur = (TT & 1) ? sb : sa;
@@ -957,7 +965,7 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
       // compiler's own interleaving: pinning one MFMA between every two
       // exponentials with scheduling-group barriers ran 0.8% slower)
       gemm0(snext);
-      probs_fast(scur, pb, shift);
+      probs_fast(scur, pb);
       pp_barrier();
       // I1: V(t) to registers, copy of K(t+4); K(t+2) complete after the wait
       load_v(vslot(ic<TT>()));
@@ -968,9 +976,11 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
       gemm1(pb);
       mask(snext, (t + 1) * kPK);
       pp_barrier();
-      // I3: K(t+2) to registers, copy of V(t+3); V(t+1) complete after the wait
+      // I3: K(t+2) to registers, copy of V(t+3); V(t+1) complete after the
+      // wait; rows whose sum reached 2^kHeadroom rebased
       load_k(kslot(ic<TT + 2>()));
       dma_v(vslot(ic<TT + 3>()), t + 3);
+      if (__builtin_amdgcn_ballot_w64(!(l < exp2f(kHeadroom))) != 0) rebase();
       wait_vm<4>();
       pp_barrier();
     };
@@ -1008,8 +1018,8 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
     }
     if (grp == 0) pp_barrier();
     wait_vm<0>();  // no copy may land in LDS after the workgroup ends
-    // a P at or above 2^kHeadroom makes the lane's sum reach it
-    ovf = !(l < exp2f(kHeadroom));
+    // every tile's sums were rebased below 2^kHeadroom (or flagged)
+    ovf = ovf || !(l < exp2f(kHeadroom));
     if (ovf) ovf_any = 1;
     __syncthreads();
     if (ovf_any) {
@@ -1114,18 +1124,19 @@ __global__ void __launch_bounds__(kThreads, 1) attn_pp_kernel(AttnParams p) {
 // held were consumed.  The operand arrangement and the slow pass are those
 // of attn_fwd_kernel.
 //
-// Softmax in this kernel takes the fewest vector instructions in L0, where
-// the exponentials already fill the SIMD's vector unit: Q is scaled by
-// c = scale * log2(e) once when it is loaded (rounded to bf16), so the S
-// product yields log2-domain scores and no per-score multiply is left.  A
-// row's reference m (its first tile's maximum) is fixed, so P may carry any
-// per-row factor: a wave whose rows all have m in [kNoShiftLo, kNoShiftHi]
-// takes P = 2^S with no subtraction at all (a scalar branch skips it), any
-// other wave P = 2^(S - m).  Each keeps P below 2^kHeadroom unless a later
-// key scores that far above its reference (0 or m), which the row sum shows
-// once at the end (any such P makes the sum reach the bound); the row sum
-// is one chain of v_dot2c_f32_bf16 into the running sum.  Against per-score
-// FMA, per-tile sums and checks, config 2 ran 6% faster.
+// Softmax (both head_dim-128 kernels): P = 2^(S*c - m) in fp32 from the
+// exact bf16 products (scaling Q by c in bf16 instead would move a score by
+// ~2^-9 |q| |k|, several times P's own rounding for keys of large norm),
+// with each row's reference m fixed at its first tile's maximum; the row
+// sum is one chain of v_dot2c_f32_bf16 into the running sum.  After each
+// tile's P*V product a ballot over the sums finds rows whose sum reached
+// 2^kHeadroom (a key that far above the reference): only those rows rescale
+// O and their sums by an exact power of two and raise m (rebase); the
+// workgroup recomputes in the slow pass only when a sum reached
+// 2^kRebaseMax or is not finite.  Against per-tile partial sums and
+// per-tile checks, config 2 ran 2% faster; a row with a key 70 log2 units
+// above its first tile costs one rebase instead of a recompute of its
+// workgroup.
 constexpr int kP3Waves = 12;
 constexpr int kP3Threads = 64 * kP3Waves;
 constexpr int kP3Rows = 32 * kP3Waves;
@@ -1219,13 +1230,6 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   // which cannot see the copies, then has no load of its own pending in the
   // key loop, where a wait for one would also wait for every copy in flight
   wait_vm<0>();
-  // Q scaled by c = softmax scale * log2(e) once and rounded to bf16, so the
-  // S product gives log2-domain scores (the rounding moves a score by about
-  // 2^-9 of |c q . k| / sqrt(D), a tenth of P's own bf16 rounding)
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qr[s][j] = static_cast<__bf16>(static_cast<float>(qr[s][j]) * c);
   f32x16 o[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -1333,29 +1337,25 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
     float mq[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) mq[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
-    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+    return half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c;
   };
-  // slow pass: P = 2^(S - m), returns the lane's sum
+  // slow pass: P = 2^(S*c - m), returns the lane's sum
   auto probs = [&](const f32x16 &s, float mr, bf16x8 (&pb)[2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj)
-        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj] - mr));
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -mr)));
     return bf16x8_sum(pb[0], 0.0f) + bf16x8_sum(pb[1], 0.0f);
   };
-  // fast pass: P = 2^(S - m) (shift) or 2^S, added to the running sum;
-  // shift is uniform over the wave, so this is a scalar branch
-  auto probs_fast = [&](f32x16 &s, bf16x8 (&pb)[2], bool shift) {
-    if (shift) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] -= m;
-      asm volatile("" : "+v"(s));
-    }
+  // fast pass: P = 2^(S*c - m) against the row's reference m, added to the
+  // running sum (one chain of dot products)
+  auto probs_fast = [&](const f32x16 &s, bf16x8 (&pb)[2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(s[8 * ks + jj]));
+      for (int jj = 0; jj < 8; ++jj)
+        pb[ks][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[8 * ks + jj], c, -m)));
     l = bf16x8_acc(pb[1], bf16x8_acc(pb[0], l));
   };
   // end of an interval: this wave's copies older than its 4 newest are
@@ -1390,13 +1390,8 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
       mask(s, 0);
       m = tile_max(s);  // finite: the first tile holds key 0
     }
-    // The reference m of a row is fixed, so P may carry any per-row factor:
-    // a wave whose rows all have m in [kNoShiftLo, kNoShiftHi] takes P = 2^S
-    // itself (no subtraction; keys whose 2^S underflows weigh below 2^-86
-    // of the row's first-tile maximum), every other wave P = 2^(S - m).
-    // Either way P < 2^kHeadroom unless a later key scores that far above
-    // the reference (0 or m), which the row sum shows at the end.
-    const bool shift = __builtin_amdgcn_ballot_w64(wave_rows && !(m >= kNoShiftLo && m <= kNoShiftHi)) != 0;
+    // P < 2^kHeadroom unless a later key scores that far above the row's
+    // reference, which its sum shows after the tile (rebase)
     // group g runs two intervals behind group g - 1
     for (int i = 0; i < grp; ++i) {
       step();
@@ -1404,11 +1399,31 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
     }
 
     bf16x8 pb[2];
+    // A row whose sum reached 2^kHeadroom met a key that far above its
+    // reference: after the tile's P*V product both lanes of the row scale O
+    // and their sums by the larger sum's power of two (exact) and raise the
+    // row's reference by as much.  A sum at or above 2^kRebaseMax, or not
+    // finite, leaves the workgroup to the slow pass.
+    auto rebase = [&]() {
+      const float lmax = half_max(l);
+      if (!(lmax < exp2f(kRebaseMax))) {
+        ovf = true;
+      } else if (!(lmax < exp2f(kHeadroom))) {
+        const int e = __builtin_amdgcn_frexp_expf(lmax);
+        const float f = __builtin_amdgcn_ldexpf(1.0f, -e);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= f;
+        l *= f;
+        m += static_cast<float>(e);
+      }
+    };
     auto iter = [&](auto tt_c, int t) {
       constexpr int TT = decltype(tt_c)::value;
       // L0: P(t)
       mask(s, t * kPK);
-      probs_fast(s, pb, shift);
+      probs_fast(s, pb);
       // the row sums are taken here, not sunk to a later interval where P
       // would have to stay live
       asm volatile("" : "+v"(l));
@@ -1420,8 +1435,9 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
       // L2: O += V(t)^T P(t)
       gemm1(pb);
       step();
-      // L3: copy of V(t+3)
+      // L3: copy of V(t+3); rows whose sum reached 2^kHeadroom rebased
       if (copier) dma_v(vslot(ic<TT + 3>()), t + 3);
+      if (__builtin_amdgcn_ballot_w64(!(l < exp2f(kHeadroom))) != 0) rebase();
       step();
       // L4: K(t+1) fragments, copy of K(t+4)
       load_k_half(kslot(ic<TT + 1>()), ic<0>());
@@ -1467,9 +1483,9 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
       step();
     }
     wait_vm<0>();  // no copy may land in LDS after the workgroup ends
-    // a P at or above 2^kHeadroom makes the lane's sum reach it
-    ovf = !(l < exp2f(kHeadroom));
-    ref = shift ? m : 0.0f;
+    // every tile's sums were rebased below 2^kHeadroom (or flagged)
+    ovf = ovf || !(l < exp2f(kHeadroom));
+    ref = m;
     if (ovf) ovf_any = 1;
     __syncthreads();
     if (ovf_any) {

@@ -434,15 +434,12 @@ def test_attention_large_launch_keys_outscoring_the_first_tile_vs_float64():
 @pytest.mark.parametrize("B", [86, 20])
 def test_attention_reference_modes_vs_float64(B):
     """Both head_dim-128 kernels (86 x 12 pairs: the 12-wave kernel; 20 x 12:
-    the 8-wave one) fix each row's reference at its first key tile.
-    A wave whose rows' first-tile maxima (log2 units) all lie in [-40, 24]
-    takes P = 2^S unshifted, any other wave P = 2^(S - m); either falls back
-    to the moving-maximum pass when a later key outscores the reference by
-    2^64.  Query rows are scaled by 1, 2 or 4 and each sequence's first tile
-    set to a constant, so that the maxima fall inside the window, above it
-    (up to ~196), below it (to ~-65, where later keys then lie past the
-    headroom) and on both sides within one wave; spiked later keys reach
-    ~98 units in unshifted rows."""
+    the 8-wave one) fix each row's reference at its first key tile's maximum.
+    Query rows are scaled by 1, 2 or 4 and each sequence's first tile set to
+    a constant, so that the references lie near 0, far above (up to ~196 log2
+    units) and far below it (to ~-65, where the later keys then lie past the
+    headroom), differing between the rows of one wave; spiked later keys
+    reach ~98 units above the reference."""
     rng = np.random.default_rng(17)
     q, k, v, cu_q, cu_k = _large_launch_case(rng, True, B=B)
     alpha = np.array([1.0, 2.0, 4.0], np.float32)[np.arange(q.shape[0]) % 3]
@@ -455,6 +452,37 @@ def test_attention_reference_modes_vs_float64(B):
         if s_ % 7 == 3 and lk[s_] > 40:
             k[cu_k[s_] + lk[s_] - 1] = O.f32_to_bf16(np.full(128, 1.5, np.float32))
     _attn_check(q, k, v, cu_q, cu_k, B, 12)
+
+
+@pytest.mark.parametrize("B", [86, 20])
+def test_attention_row_rebase_vs_float64(B):
+    """Keys aligned with single query rows, past the first key tile, scoring
+    ~70 or ~85 log2 units above the rest (those rows rescale O and their sum
+    in place after the tile and raise their reference) or ~110 (past the
+    rebase bound: the workgroup's slow pass), in sequences whose first tile
+    scores ~0 and ~40 for their first row.  Other rows meet the spiked keys
+    as distractors of large norm.  Both head_dim-128 kernels."""
+    rng = np.random.default_rng(29)
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, True, B=B)
+    H = 12
+    c = 128 ** -0.5 * 1.4426950408889634
+    qf = O.bf16_to_f32(q)
+    lk = np.diff(cu_k)
+    # rows of the first batches: a third get a first tile of constant keys scoring ~40 (shift mode)
+    for s_ in range(len(lk)):
+        b, h = divmod(s_, H)
+        if lk[s_] < 40 or np.diff(cu_q)[b] == 0:
+            continue
+        rows = np.arange(cu_q[b], cu_q[b + 1])
+        if s_ % 3 == 1:
+            qr = qf[rows[0], h]
+            k[cu_k[s_]:cu_k[s_] + 32] = O.f32_to_bf16(np.tile(qr * (40.0 / (c * float(qr @ qr))), (32, 1)))
+        units = [70.0, 85.0, 110.0][s_ % 3]
+        for j, r in enumerate(rows[:: max(1, len(rows) // 3)][:3]):
+            pos = 33 + (7 * j + s_) % max(1, lk[s_] - 33)
+            qr = qf[r, h]
+            k[cu_k[s_] + pos] = O.f32_to_bf16(qr * (units / (c * float(qr @ qr))))
+    _attn_check(q, k, v, cu_q, cu_k, B, H)
 
 
 def test_attention_rejects_causal_and_bad_head_dim():
