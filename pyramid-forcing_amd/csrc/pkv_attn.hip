@@ -1148,6 +1148,225 @@ constexpr int kPartFloats = kPartOFloats + kP3Waves * 64 * 2;
 
 static_assert(kP3Rows == kSplitRows, "a key-split item is one attn_p3_kernel workgroup");
 
+// A sequence's last query tile holds Lq mod 384 rows -- 72 of the 4,680 of a
+// rollout's query chunk -- so in the plain work shape three of its twelve
+// waves have rows, and the tile took 82% of a full workgroup's time for 19%
+// of its work.  Tiles of at most kTailRows rows instead split their keys
+// within the workgroup: wave w takes row block w >> 2 (32 rows) against key
+// quarter w & 3, so each SIMD runs one quarter's keys for up to three row
+// blocks.  Each quarter streams its tiles through its own two K and two V
+// slots (copies issued one tile ahead by waves 0-7: wave w < 4 copies the K
+// tiles of quarter w, wave 4 + w its V tiles), with the classic online
+// softmax (moving maximum; O rescaled only when a row's maximum grows, so
+// no slow pass).  Quarters 1-3 then hand (O, m, l) through LDS to quarter
+// 0, which merges them and writes the rows.
+constexpr int kTailRows = 96;
+constexpr int kTailMinTiles = 8;
+
+__device__ __attribute__((always_inline)) inline void tail_item(const AttnParams &p, uint16_t *kv,
+                                                                const uint16_t *qp, const uint16_t *kp,
+                                                                const uint16_t *vp, int q_begin, int Lq, int q0,
+                                                                int h, int Lk) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qtr = wave & 3, rb = wave >> 2;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int row_q = q0 + rb * 32 + lq;
+  const bool rows = q0 + rb * 32 < Lq;
+  const float c = p.scale_log2;
+  const int nT = (Lk + kPK - 1) / kPK;
+  // this SIMD's key quarter and the length of the longest
+  const int t_lo = qtr * nT / 4, t_hi = (qtr + 1) * nT / 4;
+  const int len = (nT + 3) / 4;
+  const int kq0 = t_lo * kPK;
+  const int Lkq = min(t_hi * kPK, Lk) - kq0;
+  auto slot = [&](int q, int kind, int j) { return kv + ((q * 2 + kind) * 2 + j) * kPTileElems; };
+
+  bf16x8 qr[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row_q < Lq) v = ldg16(qp + static_cast<int64_t>(row_q) * p.q_tok + 16 * s + 8 * hf);
+    qr[s] = as_bf16x8(v);
+  }
+  wait_vm<0>();
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  // copies: wave w < 8 copies the K (w < 4) or V (w >= 4) tiles of quarter
+  // w & 3, all 32 rows (8 instructions of 4 rows), into slot j
+  const bool copier = wave < 8;
+  const int cq = wave & 3, ckind = wave >> 2;
+  const int c_lo = cq * nT / 4, c_hi = (cq + 1) * nT / 4;
+  const int64_t row_elems = p.kv_tok;
+  const int row_bytes = static_cast<int>(row_elems) * 2;
+  const uint16_t *cbase = (ckind ? vp : kp) + static_cast<int64_t>(c_lo) * kPK * row_elems;
+  const int cLk = min(c_hi * kPK, Lk) - c_lo * kPK;
+  const int drow = lane >> 4, dpos = lane & 15;
+  auto copy_tile = [&](int i, int j) {
+    const int64_t first = static_cast<int64_t>(i) * kPK;
+    const int64_t left = (static_cast<int64_t>(cLk) - first) * row_elems * 2;
+    const int nrec = static_cast<int>(left <= 0 ? 0 : (left < 0x7fffffff ? left : 0x7fffffff));
+    const uint64_t addr = reinterpret_cast<uint64_t>(cbase + (left <= 0 ? 0 : first * row_elems));
+    i32x4 rsrc;
+    rsrc[0] = static_cast<int>(addr & 0xffffffffu);
+    rsrc[1] = static_cast<int>((addr >> 32) & 0xffffu);
+    rsrc[2] = nrec;
+    rsrc[3] = kRsrcWord3;
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)slot(cq, ckind, j)));
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) {
+      const int r = 4 * ch + drow;
+      const int sw = ckind ? (dpos ^ (4 * (r & 3))) : (dpos ^ (r & 15));
+      const int voff = r * row_bytes + 16 * sw;
+      const uint32_t lds = lds0 + ch * 4 * kPRow;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                   :
+                   : "s"(lds), "v"(voff), "s"(rsrc)
+                   : "memory", "m0");
+#pragma clang diagnostic pop
+    }
+  };
+
+  // fragment reads (the main kernel's addressing, on this quarter's slots)
+  int kaddr[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) kaddr[s] = lq * kPRow + 16 * ((2 * s + hf) ^ (lq & 15));
+  const int v_row = 4 * hf + ((lane & 15) >> 2);
+  const int v_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int vaddr[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+    vaddr[db] = v_row * kPRow + 16 * ((4 * db + v_col / 8) ^ (4 * (v_row & 3))) + 2 * (v_col % 8);
+
+  if (copier) copy_tile(0, 0);
+  for (int i = 0; i < len; ++i) {
+    const int j = i & 1;
+    if (copier) {
+      if (i + 1 < len) {
+        copy_tile(i + 1, j ^ 1);
+        wait_vm<8>();  // tile i's copies complete, tile i + 1's in flight
+      } else {
+        wait_vm<0>();
+      }
+    }
+    __syncthreads();
+    if (rows && i < t_hi - t_lo) {
+      const uint16_t *ks = slot(qtr, 0, j), *vs = slot(qtr, 1, j);
+      uint4 kreg[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        kreg[s] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(ks) + kaddr[s]);
+      f32x16 sc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kreg[s]), qr[s], sc, 0, 0, 0);
+      const int kb0 = i * kPK;
+      if (kb0 + kPK > Lkq) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (kb0 + 8 * (e / 4) + 4 * hf + (e % 4) >= Lkq) sc[e] = -INFINITY;
+      }
+      float mq[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mq[r] = fmaxf(fmaxf(sc[r], sc[r + 4]), fmaxf(sc[r + 8], sc[r + 12]));
+      const float m_new = fmaxf(m, half_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * c);
+      if (__builtin_amdgcn_ballot_w64(m_new > m) != 0) {  // some row's maximum grew
+        const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+        l *= alpha;
+        m = m_new;
+      }
+      bf16x8 pb[2];
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          pb[ks2][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(sc[8 * ks2 + jj], c, -m)));
+      l = bf16x8_acc(pb[1], bf16x8_acc(pb[0], l));
+      i16x4 vreg[2][4][2];
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const uint16_t *ptr = reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(vs) + vaddr[db] +
+                                                                   ks2 * 16 * kPRow);
+          vreg[ks2][db][0] = lds_tr16(ptr);
+          vreg[ks2][db][1] = lds_tr16(ptr + 8 * kPRow / 2);
+        }
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const i16x4 a8[2] = {vreg[ks2][db][0], vreg[ks2][db][1]};
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a8), pb[ks2], o[db], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // slot j is free for tile i + 2
+  }
+
+  // merge quarters 1-3 into quarter 0 (in quarter order, one at a time
+  // through the first 50 KB of the slots)
+  float *xo = reinterpret_cast<float *>(kv);
+  float2 *xml = reinterpret_cast<float2 *>(xo + 3 * 16 * 64 * 4);
+  for (int qq = 1; qq < 4; ++qq) {
+    if (qtr == qq && rows) {
+      float4 *po = reinterpret_cast<float4 *>(xo) + rb * 16 * 64 + lane;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        po[e * 64] = make_float4(o[e / 4][4 * (e % 4)], o[e / 4][4 * (e % 4) + 1], o[e / 4][4 * (e % 4) + 2],
+                                 o[e / 4][4 * (e % 4) + 3]);
+      xml[rb * 64 + lane] = make_float2(m, l);
+    }
+    __syncthreads();
+    if (qtr == 0 && rows) {
+      const float2 ml = xml[rb * 64 + lane];
+      const float M = fmaxf(m, ml.x);
+      const float a0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+      const float a1 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
+      const float4 *po = reinterpret_cast<const float4 *>(xo) + rb * 16 * 64 + lane;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float4 v = po[e * 64];
+        o[e / 4][4 * (e % 4)] = fmaf(o[e / 4][4 * (e % 4)], a0, v.x * a1);
+        o[e / 4][4 * (e % 4) + 1] = fmaf(o[e / 4][4 * (e % 4) + 1], a0, v.y * a1);
+        o[e / 4][4 * (e % 4) + 2] = fmaf(o[e / 4][4 * (e % 4) + 2], a0, v.z * a1);
+        o[e / 4][4 * (e % 4) + 3] = fmaf(o[e / 4][4 * (e % 4) + 3], a0, v.w * a1);
+      }
+      l = fmaf(l, a0, ml.y * a1);
+      m = M;
+    }
+    __syncthreads();
+  }
+  if (qtr != 0 || !rows) return;
+  const float lt = half_sum(l);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (row_q < Lq) {
+    uint16_t *orow = p.o + static_cast<int64_t>(q_begin + row_q) * p.o_tok + h * p.o_head;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + 8 * g + 4 * hf;
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<__bf16>(o[db][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4 *>(orow + d) = v;
+      }
+  }
+}
+
 // SPLIT: the workgroup runs item xcd_remap(blockIdx.x) of the key-split plan
 // (split_item): one query tile against one chunk of its sequence's keys.
 // An item whose sequence has one chunk writes O as the plain kernel does;
@@ -1162,7 +1381,8 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   // LDS, so that every fragment read addresses its slot by an immediate
   // offset; the work-list scratch of the prologue shares it (no copy is
   // issued before the work list is read)
-  __shared__ __attribute__((aligned(16))) uint16_t kv[8 * kPTileElems];
+  // (a tail item uses sixteen slots: its own K and V pairs per key quarter)
+  __shared__ __attribute__((aligned(16))) uint16_t kv[16 * kPTileElems];
   static_assert(8 * kPTileElems * 2 >= 6 * kSchedMax * 4, "work-list scratch fits in the tile slots");
   int *sched = reinterpret_cast<int *>(kv);
   auto kslot = [&](auto s) -> uint16_t * { return kv + (decltype(s)::value & 3) * kPTileElems; };
@@ -1218,6 +1438,13 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   const int row_q = q0 + wave * 32 + lq;
   const bool wave_rows = q0 + wave_s * 32 < Lq;
   const float c = p.scale_log2;
+
+  if constexpr (!SPLIT) {
+    if (Lq - q0 <= kTailRows && (Lk + kPK - 1) / kPK >= kTailMinTiles) {
+      tail_item(p, kv, qp, kp, vp, q_begin, Lq, q0, h, Lk);
+      return;
+    }
+  }
 
   bf16x8 qr[8];
 #pragma unroll

@@ -485,6 +485,31 @@ def test_attention_row_rebase_vs_float64(B):
     _attn_check(q, k, v, cu_q, cu_k, B, H)
 
 
+def test_attention_tail_tiles_vs_float64():
+    """The 12-wave kernel's last query tiles of at most 96 rows (a rollout's
+    72 of 4,680) split their keys in four quarters within the workgroup and
+    merge them: tails of 1, 8, 32, 33, 64, 72 and 96 rows behind full tiles
+    and alone, against key counts with quarters of unequal length, a last
+    tile of one key and tile edges; 43 x 12 pairs of up to two query tiles
+    make a launch of at least 1,024 workgroups."""
+    rng = np.random.default_rng(61)
+    B, H = 43, 12
+    tails = [1, 8, 32, 33, 64, 72, 96]
+    Lq = np.array([(384 if b % 3 else 0) + tails[b % len(tails)] for b in range(B)])
+    Lq[0] = 768  # two full tiles, no tail
+    Lk = rng.integers(256, 2000, size=B * H)
+    Lk[:6] = [256, 257, 288, 1000, 1025, 1999]
+    cu_q = np.concatenate([[0], np.cumsum(Lq)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(Lk)]).astype(np.int32)
+    q = O.f32_to_bf16((rng.standard_normal((cu_q[-1], H, 128)) * 0.5).astype(np.float32))
+    k = O.f32_to_bf16((rng.standard_normal((cu_k[-1], 128)) * 0.5).astype(np.float32))
+    v = O.f32_to_bf16((rng.standard_normal((cu_k[-1], 128)) * 0.5).astype(np.float32))
+    # a late key far above the rest in a few tails: the moving maximum rescales
+    for s_ in range(0, B * H, 17):
+        k[cu_k[s_] + Lk[s_] - 1] = O.f32_to_bf16(np.full(128, 3.0, np.float32))
+    _attn_check(q, k, v, cu_q, cu_k, B, H)
+
+
 def test_attention_rejects_causal_and_bad_head_dim():
     q = torch.zeros(4, 1, 128, dtype=torch.bfloat16, device=DEV)
     cu = torch.tensor([0, 4], dtype=torch.int32, device=DEV)
