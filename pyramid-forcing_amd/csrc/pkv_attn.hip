@@ -53,7 +53,10 @@
 // taken over the same rounded values (v_dot2c_f32_bf16 against (1, 1)), so
 // numerator and denominator use identical weights.
 
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "pkv_common.h"
 
@@ -86,6 +89,10 @@ struct AttnParams {
   float *part;
   int4 *rec;
   int n_seq, n_cu;
+  // queue launches of attn_p3_kernel<false> (one workgroup per compute
+  // unit, items claimed from per-XCD counters): this stream's counter
+  // block; null = one item per workgroup
+  int *queue;
 };
 
 // Consecutive workgroup ids are dispatched round-robin over the 8 XCDs;
@@ -176,6 +183,141 @@ __device__ bool balanced_item(const int32_t *cu_q, const int32_t *cu_k, int Hq, 
   seq_out = res[0];
   qt_out = res[1];
   return seq_out >= 0;
+}
+
+// ---- queue launches --------------------------------------------------------
+// In a launch of one workgroup per item, the dispatcher hands an XCD's
+// workgroups out in order, each to a shader engine it picks in turn; a
+// workgroup whose engine has no free compute unit holds back every later
+// one, so a unit that frees early can sit idle for tens of microseconds
+// (measured: 2.3% of every unit's time over a rollout's attention, plus the
+// ragged end of the launch).  A queue launch instead starts one workgroup
+// per compute unit; each claims items one at a time from a counter of its
+// own XCD's bin of the XCD-balanced order (the work list above, bin x =
+// what XCD x runs in a launch of one workgroup per item) and, once that bin
+// is empty, from the other bins in turn, so that units never wait on the
+// dispatcher and a slower XCD's last items go to faster ones.
+//
+// Counter block (kQueueInts ints): claims of bin x at [x], x = 0..7;
+// workgroups finished at [8].  The last workgroup to finish sets the block
+// back to zero, so consecutive launches on one stream share it.
+constexpr int kQueueInts = 32;
+
+// The work list in bin-major order: bin x holds entries [start[x],
+// start[x + 1]), each a sequence and the query tiles of the bin before it.
+struct QueueTable {
+  int seq[kSchedMax];
+  int pre[kSchedMax];
+  int start[9];
+  int total[8];
+};
+
+// Builds the table from cu_q / cu_k (every workgroup, once per launch;
+// every thread calls it).  scratch: 4 * kSchedMax ints of LDS.
+__device__ void queue_table(const int32_t *cu_q, const int32_t *cu_k, int Hq, int n_seq, int kv_per_head, int bq,
+                            int *scratch, QueueTable &tab) {
+  int *cost = scratch, *order = scratch + kSchedMax, *qts = scratch + 2 * kSchedMax, *tq = scratch + 3 * kSchedMax;
+  const int n4 = (n_seq + 3) & ~3;
+  for (int s = threadIdx.x; s < n4; s += blockDim.x) {
+    int nq = 0, cs = -1;  // padding entries rank after every sequence
+    if (s < n_seq) {
+      const int b = s / Hq;
+      nq = (cu_q[b + 1] - cu_q[b] + bq - 1) / bq;
+      const int kv = kv_per_head ? s : b;
+      cs = nq * ((cu_k[kv + 1] - cu_k[kv] + 63) / 64 + 1);  // the cost balanced_item ranks by
+    }
+    qts[s] = nq;
+    cost[s] = cs;
+  }
+  if (threadIdx.x < 9) {
+    // bin x: one entry per full row of 8 ranks, and one in the last, partial
+    // row when the snake order reaches it (rows run 0..7 and 7..0 in turn)
+    const int rows = n_seq >> 3, rem = n_seq & 7;
+    int st = 0;
+    for (int x = 0; x < static_cast<int>(threadIdx.x); ++x) st += rows + ((rows & 1) ? (7 - x < rem) : (x < rem));
+    tab.start[threadIdx.x] = st;
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < n_seq; s += blockDim.x) {
+    const int cs = cost[s];
+    int r = 0;
+    const int4 *c4 = reinterpret_cast<const int4 *>(cost);
+#pragma unroll 4
+    for (int t4 = 0; t4 < n4 / 4; ++t4) {
+      const int4 v = c4[t4];
+      const int t = 4 * t4;
+      r += (v.x > cs) || (v.x == cs && t < s);
+      r += (v.y > cs) || (v.y == cs && t + 1 < s);
+      r += (v.z > cs) || (v.z == cs && t + 2 < s);
+      r += (v.w > cs) || (v.w == cs && t + 3 < s);
+    }
+    order[r] = s;
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < n_seq; r += blockDim.x) {
+    const int e = tab.start[snake_bin(r)] + (r >> 3);
+    tab.seq[e] = order[r];
+    tq[e] = qts[order[r]];
+  }
+  __syncthreads();
+  if (threadIdx.x < 8) {
+    int run = 0;
+    for (int e = tab.start[threadIdx.x]; e < tab.start[threadIdx.x + 1]; ++e) {
+      tab.pre[e] = run;
+      run += tq[e];
+    }
+    tab.total[threadIdx.x] = run;
+  }
+  __syncthreads();
+}
+
+// Claims the next item (thread 0; the result reaches every thread): from
+// this XCD's bin, else from bins x + 1, x + 2, ... (mod 8).  `spent` (thread
+// 0's) holds the bins found empty.  The first barrier also ends the last
+// item: no wave still reads its tiles when the next item's copies begin.
+__device__ bool queue_next(int *queue, const QueueTable &tab, unsigned &spent, int &seq, int &qt) {
+  __shared__ int pick[2];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int sq = -1, t = 0;
+    const int x = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 7;  // HW_REG_XCC_ID, bits 3:0
+    for (int d = 0; d < 8 && sq < 0; ++d) {
+      const int y = (x + d) & 7;
+      if (spent & (1u << y)) continue;
+      const int n_y = tab.total[y];
+      const int i = n_y > 0 ? __hip_atomic_fetch_add(queue + y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+      if (i >= n_y) {
+        spent |= 1u << y;
+        continue;
+      }
+      // the bin's last entry whose tiles start at or before item i
+      int lo = tab.start[y], hi = tab.start[y + 1] - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tab.pre[mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      sq = tab.seq[lo];
+      t = i - tab.pre[lo];
+    }
+    pick[0] = sq;
+    pick[1] = t;
+  }
+  __syncthreads();
+  seq = pick[0];
+  qt = pick[1];
+  return seq >= 0;
+}
+
+// Counts the workgroup out; the last one clears the counters for the next
+// launch on the stream (its acquire sees every other workgroup's claims).
+__device__ void queue_done(int *queue) {
+  if (threadIdx.x == 0) {
+    const int d = __hip_atomic_fetch_add(queue + 8, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == static_cast<int>(gridDim.x) - 1) {
+      for (int y = 0; y < 9; ++y) __hip_atomic_store(queue + y, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // One item of a key-split launch: query tile qt of sequence seq against key
@@ -1155,8 +1297,10 @@ static_assert(kP3Rows == kSplitRows, "a key-split item is one attn_p3_kernel wor
 // within the workgroup: wave w takes row block w >> 2 (32 rows) against key
 // quarter w & 3, so each SIMD runs one quarter's keys for up to three row
 // blocks.  Each quarter streams its tiles through its own two K and two V
-// slots (copies issued one tile ahead by waves 0-7: wave w < 4 copies the K
-// tiles of quarter w, wave 4 + w its V tiles), with the classic online
+// slots (waves 0-7 copy: wave w < 4 the K tiles of quarter w, wave 4 + w
+// its V tiles; K runs a tile ahead of V, so that a step's score MFMAs are
+// those of the next tile and overlap its softmax, and one-dword touches
+// four tiles ahead bring the keys into L2), with the classic online
 // softmax (moving maximum; O rescaled only when a row's maximum grows, so
 // no slow pass).  Quarters 1-3 then hand (O, m, l) through LDS to quarter
 // 0, which merges them and writes the rows.
@@ -1167,7 +1311,10 @@ __device__ __attribute__((always_inline)) inline void tail_item(const AttnParams
                                                                 const uint16_t *qp, const uint16_t *kp,
                                                                 const uint16_t *vp, int q_begin, int Lq, int q0,
                                                                 int h, int Lk) {
-  const int tid = threadIdx.x;
+  // opaque per item: nothing derived from the lane is hoisted out of a queue
+  // launch's item loop (where it would stay live through every item)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qtr = wave & 3, rb = wave >> 2;
   const int lq = lane & 31, hf = lane >> 5;
@@ -1234,40 +1381,84 @@ __device__ __attribute__((always_inline)) inline void tail_item(const AttnParams
     }
   };
 
-  // fragment reads (the main kernel's addressing, on this quarter's slots)
-  int kaddr[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) kaddr[s] = lq * kPRow + 16 * ((2 * s + hf) ^ (lq & 15));
+  // fragment reads (the main kernel's addressing, on this quarter's slots).
+  // K chunk 2s + hf of row lq sits at 16 * ((2s + hf) ^ (lq & 15)) within
+  // the row, which is kaddr0 ^ (s << 5); the V transpose reads of column
+  // block db sit at vaddr0 ^ (db << 6).  Both are recomputed every step
+  // from bases the compiler cannot hoist, which keeps twelve addresses out
+  // of the registers.
+  const int kaddr0 = lq * kPRow + 16 * (hf ^ (lq & 15));
   const int v_row = 4 * hf + ((lane & 15) >> 2);
   const int v_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  int vaddr[4];
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-    vaddr[db] = v_row * kPRow + 16 * ((4 * db + v_col / 8) ^ (4 * (v_row & 3))) + 2 * (v_col % 8);
+  const int vaddr0 = v_row * kPRow + 16 * ((v_col / 8) ^ (4 * (v_row & 3))) + 2 * (v_col % 8);
+  static_assert(kPRow == 256, "the XOR forms assume 256-byte rows");
 
-  if (copier) copy_tile(0, 0);
-  for (int i = 0; i < len; ++i) {
-    const int j = i & 1;
-    if (copier) {
-      if (i + 1 < len) {
-        copy_tile(i + 1, j ^ 1);
-        wait_vm<8>();  // tile i's copies complete, tile i + 1's in flight
-      } else {
-        wait_vm<0>();
-      }
+  // touch: one dword per 64 bytes of tile i of this wave's quarter and kind,
+  // copied into a 256-byte LDS sink that nothing reads, so that the tile is
+  // in L2 when its copy is issued (the quarters read keys that the
+  // sequence's other query tiles have not reached yet)
+  __shared__ __attribute__((aligned(16))) uint32_t sink[64];
+  const uint32_t sink0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)sink));
+  auto touch_tile = [&](int i) {
+    const int64_t first = static_cast<int64_t>(i) * kPK;
+    const int64_t left = (static_cast<int64_t>(cLk) - first) * row_elems * 2;
+    // always two loads (the waits count them); past the quarter's keys they
+    // have no records and read nothing
+    const int nrec = static_cast<int>(left <= 0 ? 0 : (left < 0x7fffffff ? left : 0x7fffffff));
+    const uint64_t addr = reinterpret_cast<uint64_t>(cbase + (left <= 0 ? 0 : first * row_elems));
+    i32x4 rsrc;
+    rsrc[0] = static_cast<int>(addr & 0xffffffffu);
+    rsrc[1] = static_cast<int>((addr >> 32) & 0xffffu);
+    rsrc[2] = nrec;
+    rsrc[3] = kRsrcWord3;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int voff = (16 * u + (lane >> 2)) * row_bytes + 64 * (lane & 3);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                   :
+                   : "s"(sink0), "v"(voff), "s"(rsrc)
+                   : "memory", "m0");
+#pragma clang diagnostic pop
     }
-    __syncthreads();
-    if (rows && i < t_hi - t_lo) {
-      const uint16_t *ks = slot(qtr, 0, j), *vs = slot(qtr, 1, j);
-      uint4 kreg[8];
+  };
+  // K runs one tile ahead of V: step i reads K tile i + 1 (the scores of
+  // the next step, whose MFMAs overlap this step's softmax) and V tile i,
+  // while the copies of K tile i + 2 and V tile i + 1 fill the other slots
+  auto scores = [&](const uint16_t *ks) {
+    int ka = kaddr0;
+    asm volatile("" : "+v"(ka));
+    uint4 kreg[8];
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
-        kreg[s] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(ks) + kaddr[s]);
-      f32x16 sc;
+    for (int s = 0; s < 8; ++s)
+      kreg[s] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(ks) + (ka ^ (s << 5)));
+    f32x16 sc;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
+    for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kreg[s]), qr[s], sc, 0, 0, 0);
+    for (int s = 0; s < 8; ++s) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kreg[s]), qr[s], sc, 0, 0, 0);
+    return sc;
+  };
+  const int nq = t_hi - t_lo;  // this quarter's tiles (len or len - 1)
+  if (copier) {
+    copy_tile(0, 0);
+    if (ckind == 0) copy_tile(1, 1);
+    wait_vm<0>();
+  }
+  __syncthreads();
+  f32x16 sc = {};
+  if (rows && nq > 0) sc = scores(slot(qtr, 0, 0));
+  for (int i = 0; i < len; ++i) {
+    if (copier) wait_vm<2>();  // the copies of the last step (its touches may be in flight)
+    __syncthreads();           // ... are visible, and the slots they replace are read
+    if (copier) {
+      copy_tile(ckind ? i + 1 : i + 2, ckind ? (i + 1) & 1 : i & 1);
+      touch_tile(i + 4);
+    }
+    if (rows && i < nq) {
+      const f32x16 sn = scores(slot(qtr, 0, (i + 1) & 1));  // unused past the quarter's end
+      const uint16_t *vs = slot(qtr, 1, i & 1);
       const int kb0 = i * kPK;
       if (kb0 + kPK > Lkq) {
 #pragma unroll
@@ -1294,47 +1485,54 @@ __device__ __attribute__((always_inline)) inline void tail_item(const AttnParams
         for (int jj = 0; jj < 8; ++jj)
           pb[ks2][jj] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(sc[8 * ks2 + jj], c, -m)));
       l = bf16x8_acc(pb[1], bf16x8_acc(pb[0], l));
-      i16x4 vreg[2][4][2];
+      int va = vaddr0;
+      asm volatile("" : "+v"(va));
 #pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2)
+      for (int ks2 = 0; ks2 < 2; ++ks2) {  // one key half at a time (16 registers of V fragments)
+        i16x4 vreg[4][2];
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          const uint16_t *ptr = reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(vs) + vaddr[db] +
-                                                                   ks2 * 16 * kPRow);
-          vreg[ks2][db][0] = lds_tr16(ptr);
-          vreg[ks2][db][1] = lds_tr16(ptr + 8 * kPRow / 2);
+          const uint16_t *ptr = reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(vs) +
+                                                                   (va ^ (db << 6)) + ks2 * 16 * kPRow);
+          vreg[db][0] = lds_tr16(ptr);
+          vreg[db][1] = lds_tr16(ptr + 8 * kPRow / 2);
         }
 #pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2)
-#pragma unroll
         for (int db = 0; db < 4; ++db) {
-          const i16x4 a8[2] = {vreg[ks2][db][0], vreg[ks2][db][1]};
+          const i16x4 a8[2] = {vreg[db][0], vreg[db][1]};
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a8), pb[ks2], o[db], 0, 0, 0);
         }
+      }
+      sc = sn;
     }
-    __syncthreads();  // slot j is free for tile i + 2
   }
+  if (copier) wait_vm<0>();
+  __syncthreads();  // every copy landed and every slot read: the slots hold the merge
 
   // merge quarters 1-3 into quarter 0 (in quarter order, one at a time
   // through the first 50 KB of the slots)
   float *xo = reinterpret_cast<float *>(kv);
   float2 *xml = reinterpret_cast<float2 *>(xo + 3 * 16 * 64 * 4);
+  // the lane index again, rather than keeping tid & 63 live through the loop
+  int ln = threadIdx.x;
+  asm volatile("" : "+v"(ln));
+  ln &= 63;
   for (int qq = 1; qq < 4; ++qq) {
     if (qtr == qq && rows) {
-      float4 *po = reinterpret_cast<float4 *>(xo) + rb * 16 * 64 + lane;
+      float4 *po = reinterpret_cast<float4 *>(xo) + rb * 16 * 64 + ln;
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         po[e * 64] = make_float4(o[e / 4][4 * (e % 4)], o[e / 4][4 * (e % 4) + 1], o[e / 4][4 * (e % 4) + 2],
                                  o[e / 4][4 * (e % 4) + 3]);
-      xml[rb * 64 + lane] = make_float2(m, l);
+      xml[rb * 64 + ln] = make_float2(m, l);
     }
     __syncthreads();
     if (qtr == 0 && rows) {
-      const float2 ml = xml[rb * 64 + lane];
+      const float2 ml = xml[rb * 64 + ln];
       const float M = fmaxf(m, ml.x);
       const float a0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
       const float a1 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
-      const float4 *po = reinterpret_cast<const float4 *>(xo) + rb * 16 * 64 + lane;
+      const float4 *po = reinterpret_cast<const float4 *>(xo) + rb * 16 * 64 + ln;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const float4 v = po[e * 64];
@@ -1375,42 +1573,17 @@ __device__ __attribute__((always_inline)) inline void tail_item(const AttnParams
 // maximum -- and the row sum l, per lane) to part slot c, and
 // attn_combine_kernel merges a query tile's chunks.  Every workgroup writes
 // its item's record (k = 0 when the item does not exist).
+// One work item of attn_p3_kernel: query tile qt (kP3Rows rows) of
+// sequence seq against all of its keys, or, in a key-split launch, against
+// the chunk of keys that `it` names.  Every wave takes every barrier of the
+// item; waves leave only after the item's last barrier.
 template <bool SPLIT>
-__global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
-  // the eight tile slots (K 0-3, V 4-7) in one 64 KB array at the start of
-  // LDS, so that every fragment read addresses its slot by an immediate
-  // offset; the work-list scratch of the prologue shares it (no copy is
-  // issued before the work list is read)
-  // (a tail item uses sixteen slots: its own K and V pairs per key quarter)
-  __shared__ __attribute__((aligned(16))) uint16_t kv[16 * kPTileElems];
-  static_assert(8 * kPTileElems * 2 >= 6 * kSchedMax * 4, "work-list scratch fits in the tile slots");
-  int *sched = reinterpret_cast<int *>(kv);
+__device__ __attribute__((always_inline)) inline void p3_item(const AttnParams &p, uint16_t *kv, int seq, int qt,
+                                                              const SplitItem &it) {
   auto kslot = [&](auto s) -> uint16_t * { return kv + (decltype(s)::value & 3) * kPTileElems; };
   auto vslot = [&](auto s) -> uint16_t * { return kv + (4 + (decltype(s)::value & 3)) * kPTileElems; };
   uint16_t *const Ka = kslot(ic<0>()), *const Kb = kslot(ic<1>()), *const Kc = kslot(ic<2>()), *const Kd = kslot(ic<3>());
   uint16_t *const Va = vslot(ic<0>()), *const Vb = vslot(ic<1>()), *const Vc = vslot(ic<2>());
-
-  int seq, qt;
-  SplitItem it{};
-  if constexpr (SPLIT) {
-    const int c = xcd_remap(blockIdx.x, p.n_wg);
-    const bool ok = split_item(p, p.n_wg, c, sched, it);
-    if (threadIdx.x == 0) p.rec[c] = ok ? make_int4(it.seq, it.qt, it.j | (it.k << 16), it.nq) : make_int4(0, 0, 0, 0);
-    if (!ok) return;
-    seq = it.seq;
-    qt = it.qt;
-  } else {
-    const int n_seq = p.n_wg / p.q_tiles;
-    if (n_seq <= kSchedMax) {
-      if (!balanced_item(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, kP3Rows, xcd_remap(blockIdx.x, p.n_wg), sched,
-                         seq, qt))
-        return;
-    } else {
-      const int wg = xcd_remap(blockIdx.x, p.n_wg);
-      seq = wg / p.q_tiles;
-      qt = wg % p.q_tiles;
-    }
-  }
   const int b = seq / p.Hq, h = seq % p.Hq;
   const int q_begin = p.cu_q[b];
   const int Lq = p.cu_q[b + 1] - q_begin;
@@ -1429,7 +1602,10 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   const uint16_t *kp = p.k + kv_off;
   const uint16_t *vp = p.v + kv_off;
 
-  const int tid = threadIdx.x;
+  // opaque per item: nothing derived from the lane is hoisted out of a queue
+  // launch's item loop (where it would stay live through every item)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63, wave = tid >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int grp = wave_s >> 2, wq = wave_s & 3;
@@ -1778,8 +1954,10 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
   uint16_t *op = p.o + static_cast<int64_t>(q_begin) * p.o_tok + h * p.o_head;
   const float lt = half_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  if (row_q < Lq) {
-    uint16_t *orow = op + static_cast<int64_t>(row_q) * p.o_tok;
+  int rq = row_q;  // the row's offset computed again, not kept from the Q load through the key loop
+  asm volatile("" : "+v"(rq));
+  if (rq < Lq) {
+    uint16_t *orow = op + static_cast<int64_t>(rq) * p.o_tok;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -1791,6 +1969,51 @@ __global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
         for (int e = 0; e < 4; ++e) v[e] = static_cast<__bf16>(o[db][4 * g + e] * inv);
         *reinterpret_cast<bf16x4 *>(orow + d) = v;
       }
+  }
+}
+
+template <bool SPLIT>
+__global__ void __launch_bounds__(kP3Threads, 1) attn_p3_kernel(AttnParams p) {
+  // the eight tile slots (K 0-3, V 4-7) in one 64 KB array at the start of
+  // LDS, so that every fragment read addresses its slot by an immediate
+  // offset; the work-list scratch of the prologue shares it (no copy is
+  // issued before the work list is read)
+  // (a tail item uses sixteen slots: its own K and V pairs per key quarter)
+  __shared__ __attribute__((aligned(16))) uint16_t kv[16 * kPTileElems];
+  static_assert(8 * kPTileElems * 2 >= 6 * kSchedMax * 4, "work-list scratch fits in the tile slots");
+  int *sched = reinterpret_cast<int *>(kv);
+  if constexpr (SPLIT) {
+    SplitItem it{};
+    const int c = xcd_remap(blockIdx.x, p.n_wg);
+    const bool ok = split_item(p, p.n_wg, c, sched, it);
+    if (threadIdx.x == 0) p.rec[c] = ok ? make_int4(it.seq, it.qt, it.j | (it.k << 16), it.nq) : make_int4(0, 0, 0, 0);
+    if (!ok) return;
+    p3_item<true>(p, kv, it.seq, it.qt, it);
+  } else {
+    const int n_seq = p.n_wg / p.q_tiles;
+    __shared__ QueueTable tab;
+    if (p.queue) queue_table(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, kP3Rows, sched, tab);
+    unsigned spent = 0;  // queue mode: the bins this workgroup found empty (thread 0)
+    for (bool first = true;; first = false) {
+      int seq, qt;
+      if (p.queue) {
+        if (!queue_next(p.queue, tab, spent, seq, qt)) break;
+      } else {
+        // one item per workgroup, in the XCD-balanced order
+        if (!first) break;
+        if (n_seq <= kSchedMax) {
+          if (!balanced_item(p.cu_q, p.cu_k, p.Hq, n_seq, p.kv_per_head, kP3Rows, xcd_remap(blockIdx.x, p.n_wg),
+                             sched, seq, qt))
+            break;
+        } else {
+          const int wg = xcd_remap(blockIdx.x, p.n_wg);
+          seq = wg / p.q_tiles;
+          qt = wg % p.q_tiles;
+        }
+      }
+      p3_item<false>(p, kv, seq, qt, SplitItem{});
+    }
+    if (p.queue) queue_done(p.queue);
   }
 }
 
@@ -1869,6 +2092,45 @@ static int device_cus() {
   return cus[dev];
 }
 
+// Queue counter blocks: a file-scope array on each device, kQueueSlots
+// blocks of kQueueInts ints.  A stream takes a block on its first queue
+// launch on a device (cleared there, in stream order, by a one-workgroup
+// kernel) and keeps it, so launches on one stream reuse it in turn and
+// launches on different streams never share one.  Past kQueueSlots streams
+// on a device, launches run one item per workgroup.
+constexpr int kQueueSlots = 64;
+__device__ __attribute__((aligned(256))) int g_attn_queue[kQueueSlots * kQueueInts];
+
+__global__ void queue_clear_kernel(int *q) {
+  if (threadIdx.x < kQueueInts) q[threadIdx.x] = 0;
+}
+
+static int *queue_for(hipStream_t st) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, int *> blocks;
+  static int *base[64];
+  static int used[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, st);
+  const auto found = blocks.find(key);
+  if (found != blocks.end()) return found->second;
+  if (!base[dev]) {
+    // the array's address on this device (the host-side name is not one)
+    void *ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_attn_queue)) != hipSuccess || !ptr) return nullptr;
+    base[dev] = static_cast<int *>(ptr);
+  }
+  if (used[dev] >= kQueueSlots) return nullptr;
+  int *q = base[dev] + used[dev] * kQueueInts;
+  hipLaunchKernelGGL(queue_clear_kernel, dim3(1), dim3(64), 0, st, q);
+  if (hipGetLastError() != hipSuccess) return nullptr;
+  ++used[dev];
+  blocks.emplace(key, q);
+  return q;
+}
+
 // Items a key-split launch may have: three per compute unit.
 static int64_t split_items() { return 3 * static_cast<int64_t>(device_cus()); }
 static int64_t split_ws_bytes(int64_t items) {
@@ -1888,7 +2150,7 @@ static int launch_split(const pkv_attn_args *a, void *ws, int64_t ws_bytes, hipS
   if (!ws || a->head_dim != 128 || !a->kv_per_head || n <= 0 || seqs > kSchedMax ||
       seqs * q_tiles >= kP3MinGrid || seqs * q_tiles > n || ws_bytes < split_ws_bytes(n))
     return -1;
-  AttnParams p;
+  AttnParams p{};
   p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o;
   p.cu_q = a->cu_seqlens_q; p.cu_k = a->cu_seqlens_k;
   p.Hq = a->num_heads_q;
@@ -1913,7 +2175,7 @@ static int launch_split(const pkv_attn_args *a, void *ws, int64_t ws_bytes, hipS
 template <int D>
 static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   constexpr int BQ = 32 * kWaves;
-  AttnParams p;
+  AttnParams p{};
   p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o;
   p.cu_q = a->cu_seqlens_q; p.cu_k = a->cu_seqlens_k;
   p.Hq = a->num_heads_q;
@@ -1933,7 +2195,11 @@ static int launch_attn(const pkv_attn_args *a, hipStream_t st) {
   p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
   if (p.n_wg == 0) return PKV_OK;
   if (p3) {
-    hipLaunchKernelGGL(attn_p3_kernel<false>, dim3(p.n_wg), dim3(kP3Threads), 0, st, p);
+    // a queue launch (one workgroup per compute unit) when the XCD-balanced
+    // work list covers the sequences and this stream has a counter block
+    const int cus = device_cus();
+    p.queue = seqs <= kSchedMax && cus > 0 && p.n_wg > cus ? queue_for(st) : nullptr;
+    hipLaunchKernelGGL(attn_p3_kernel<false>, dim3(p.queue ? cus : p.n_wg), dim3(kP3Threads), 0, st, p);
     return check_launch("attn_p3_kernel");
   }
   if (D == 128) {
