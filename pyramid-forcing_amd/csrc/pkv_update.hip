@@ -1984,6 +1984,390 @@ __global__ void __launch_bounds__(kUpdThreads)
 
 }
 
+// The decision words after a step (the values veil_apply gives lanes
+// kVlCount, kVlId, kVlSeen and kVlDone), for the next frame's decision
+__device__ inline void veil_advance(VeilWords &v, const VeilStep &s) {
+  if (!s.changes()) return;
+  v.count = (v.count & ~0xffu) | (static_cast<uint32_t>(s.cc) & 0xffu);
+  v.id0 = s.id0;
+  v.id1 = s.id1;
+  v.seen0 = s.seen0;
+  v.seen1 = s.seen1;
+  v.done = (v.done & 0xffff0000u) | (static_cast<uint32_t>(s.done0) & 0xffu) |
+           ((static_cast<uint32_t>(s.done1) & 0xffu) << 8);
+}
+
+// ---- Veil eviction of several frames per call (pkv_evict_merge, F > 1) ------
+//
+// Each workgroup takes one merge tile (8 groups at head_dim 128; a thread
+// is a group, K or V and an 8-wide chunk, as in update_kernel's tiles)
+// through all F frames, with its group's sums of both accumulator slots in
+// registers: a slot's sums are read once (when its first use in the call
+// continues a block) and stored once, after the last frame.  The frames'
+// patch chunks stream through a ring of kEfRing frames of non-temporal
+// loads, issued before anything is decided.  The Veil steps are decided in
+// scalar registers frame by frame (every wave, the same); a first pass
+// over them finds the slots whose first use continues a block, whose
+// stored group ids are then verified against the grid by a block-wide vote
+// (as in evict_kernel).  The head's last workgroup to arrive applies every
+// step to the record's Veil words and writes them, the descriptors and the
+// slots' group counts and weight sums.  A head this path does not cover
+// (another strategy kind or patch size, a continued block off the grid)
+// runs update_kernel's merge tile, the same in every workgroup of the
+// head.  Sums are added frame by frame and member by member, as one frame
+// per call adds them: the results equal F calls of one frame bit for bit.
+constexpr int kEfRing = 2;
+
+__global__ void __launch_bounds__(kUpdThreads)
+    evict_frames_kernel(const HeadState *states, const int64_t *t_vals, const float *weights,
+                        const int32_t *num_groups, const float *weight_sum, int32_t n_merge, int32_t mma, UpdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) int32_t dyn[];
+  __shared__ __attribute__((aligned(16))) UpdShared sh;
+  constexpr int p = kPrePatch, kTok = kPreTok;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x / n_merge, tile = blockIdx.x % n_merge;
+  const int64_t hs0 = static_cast<int64_t>(h) * mma;
+  const int F = a.F;
+
+  // one wave-wide gather: lane l < 39 reads Veil word l of the record, the
+  // next lanes the record's kind, capacity, patch and block frames and the
+  // slots' group counts and weight sums (absent inputs read a stand-in)
+  constexpr int kGKind = kVeilWords, kGCap = kGKind + 1, kGPatch = kGKind + 2, kGBf = kGKind + 3,
+                kGNg = kGKind + 4, kGWs = kGKind + 6;
+  static_assert(kGWs + 2 <= 64, "one gathered value per lane");
+  const int32_t *rec = reinterpret_cast<const int32_t *>(states + h);
+  const int32_t *gp = rec + kVeilWord0 + min(lane, kVeilWords - 1);
+  const int s1 = min(1, mma - 1);
+  if (lane == kGKind) gp = rec;
+  if (lane == kGCap) gp = rec + offsetof(HeadState, capacity) / 4;
+  if (lane == kGPatch) gp = rec + offsetof(HeadState, patch_size) / 4;
+  if (lane == kGBf) gp = rec + offsetof(HeadState, block_frames) / 4;
+  if (lane == kGNg || lane == kGNg + 1) gp = num_groups + hs0 + (lane == kGNg ? 0 : s1);
+  if ((lane == kGWs || lane == kGWs + 1) && weight_sum)
+    gp = reinterpret_cast<const int32_t *>(weight_sum + hs0 + (lane == kGWs ? 0 : s1));
+  uint32_t rw = static_cast<uint32_t>(*gp);
+  // frame f's time and weight in lane f (read with readlane: no load, and
+  // so no wait, in the frame loop, whose waits would also wait for the
+  // frames in flight)
+  static_assert(kUpdMaxFrames <= 64, "one frame per lane");
+  const int64_t t_lane = t_vals[min(lane, F - 1)];
+  const float w_lane = weights ? weights[min(lane, F - 1)] : 1.0f;
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int FSEQ = a.FSEQ, D = a.D, MTPA = a.MTPA, W = a.width;
+  const int cols = W / p, grid_ng = FSEQ / (p * p);
+  const pkv_merge_layer &ml = a.ml;
+  const MergeLane ln(a, tile);
+  const int g = ln.g, c = ln.c, is_v = uni(ln.is_v);  // wave-uniform: a scalar buffer resource, no per-lane loop
+  const bool own = ln.own;
+  const bool meta_lane = own && !is_v && c == 0;  // writes the group's count and positions
+  // the group's members in every frame, copied into this wave's ring
+  // slots in LDS (the dynamic LDS, which only the fallback path uses
+  // otherwise): slot r of wave w holds member m of every lane at
+  // ((r * 4 + w) * kTok + m) * 1 KB, lane l at +16 l.  One buffer resource
+  // over the head's rows of all F frames (32-bit offsets).
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 srsrc;
+  {
+    const uint64_t addr = reinterpret_cast<uint64_t>(reinterpret_cast<const char *>(is_v ? a.src.v : a.src.k) +
+                                                     static_cast<uint64_t>(h) * a.src_hb);
+    srsrc[0] = static_cast<int>(addr & 0xffffffffu);
+    srsrc[1] = static_cast<int>((addr >> 32) & 0xffffu);
+    srsrc[2] = static_cast<int>(static_cast<int64_t>(F - 1) * a.src_fb + static_cast<int64_t>(FSEQ - 1) * a.src_tb +
+                                D * 2);
+    srsrc[3] = kRsrcWord3;
+  }
+  uint32_t toff[kTok];
+  {
+    const int gc = min(g, grid_ng - 1);
+    const int gbase = (gc / cols) * p * W + (gc % cols) * p;
+#pragma unroll
+    for (int m = 0; m < kTok; ++m) toff[m] = c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb;
+  }
+  const int wave_s = uni(wave);
+  typedef __attribute__((address_space(3))) char lds_char_t;
+  const uint32_t ring0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char_t *)dyn));
+  // frame f (the last frame past the end) into ring slot r: kTok copies
+  auto copy_frame = [&](int f, int r) {
+    const uint32_t fo = static_cast<uint32_t>(min(f, F - 1)) * a.src_fb;
+#pragma unroll
+    for (int m = 0; m < kTok; ++m) {
+      const uint32_t lds = ring0 + static_cast<uint32_t>(((r * 4 + wave_s) * kTok + m) * 1024);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                   :
+                   : "s"(lds), "v"(fo + toff[m]), "s"(srsrc)
+                   : "memory", "m0");
+#pragma clang diagnostic pop
+    }
+  };
+  auto ring_read = [&](int r, int m) {
+    return *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(dyn) +
+                                            ((r * 4 + wave_s) * kTok + m) * 1024 + lane * 16);
+  };
+#pragma unroll
+  for (int r = 0; r < kEfRing; ++r) copy_frame(r, r);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int32_t kind = static_cast<int8_t>(lane_word(rw, kGKind) & 0xff);
+  const int32_t cap = lane_word(rw, kGCap), pch = lane_word(rw, kGPatch), bf = lane_word(rw, kGBf);
+  const int32_t ng0 = lane_word(rw, kGNg), ng1 = lane_word(rw, kGNg + 1);
+  const float ws0 = weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs)) : 0.0f;
+  const float ws1 = weight_sum ? __builtin_bit_cast(float, lane_word(rw, kGWs + 1)) : 0.0f;
+  VeilWords vw;
+  vw.count = static_cast<uint32_t>(lane_word(rw, kVlCount));
+  vw.id0 = lane_word(rw, kVlId);
+  vw.id1 = lane_word(rw, kVlId + 1);
+  vw.seen0 = static_cast<uint32_t>(lane_word(rw, kVlSeen));
+  vw.seen1 = static_cast<uint32_t>(lane_word(rw, kVlSeen + 1));
+  vw.done = static_cast<uint32_t>(lane_word(rw, kVlDone));
+  const bool veil = kind == SK_MERGE && pch == p;
+
+  auto frame_t = [&](int f) {
+    const uint64_t u = static_cast<uint64_t>(t_lane);
+    return static_cast<int64_t>(
+        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), f))) << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), f)));
+  };
+  auto frame_w = [&](int f) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_lane), f)); };
+
+  // the slots whose first use in the call continues a block: only a slot
+  // holding a block at the start can, so the steps are followed only until
+  // each such slot's first use is known
+  uint32_t cont = 0;
+  if (veil) {
+    VeilWords v = vw;
+    uint32_t open = (vw.id0 != -1 ? 1u : 0u) | (vw.id1 != -1 && mma > 1 ? 2u : 0u);
+    for (int f = 0; f < F && open; ++f) {
+      const VeilStep s = veil_decide(v, bf, cap, static_cast<int32_t>(frame_t(f)));
+      veil_advance(v, s);
+      const int sl = s.d.accum_slot;
+      if (!s.changes() || sl < 0 || sl >= mma || !(open & (1u << sl))) continue;
+      if (!s.d.is_new_block) cont |= 1u << sl;
+      open &= ~(1u << sl);
+    }
+  }
+
+  // arrival as soon as every wave holds its gather (evict_kernel's
+  // protocol): no workgroup of the head reads the record, the slot counts
+  // or the weight sums after it; the stored group ids read below are
+  // rewritten in this call only with the grid's ids, which they hold
+  __syncthreads();
+  int early = 0;
+  if (tid == 0) early = atomicAdd(a.early + static_cast<int64_t>(h) * kArriveStride, 1);
+
+  float ax[2][8];
+  int64_t apos[2][3] = {};
+  bool fast = veil;
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ax[sl][e] = 0.0f;
+    if (!(cont & (1u << sl))) continue;
+    const int64_t hs = hs0 + sl;
+    int4 ids[kEvIdLoads];
+    const int n4 = FSEQ / 4;
+#pragma unroll
+    for (int k = 0; k < kEvIdLoads; ++k)
+      ids[k] = reinterpret_cast<const int4 *>(ml.accum_group_ids + hs * FSEQ)[min(tid + k * kUpdThreads, n4 - 1)];
+    const float *acc_sum = is_v ? ml.accum_sum_v : ml.accum_sum_k;
+    const float4 *ap = reinterpret_cast<const float4 *>(acc_sum + (hs * MTPA + min(g, MTPA - 1)) * D + c);
+    const float4 a0 = ap[0], a1 = ap[1];
+    ax[sl][0] = a0.x; ax[sl][1] = a0.y; ax[sl][2] = a0.z; ax[sl][3] = a0.w;
+    ax[sl][4] = a1.x; ax[sl][5] = a1.y; ax[sl][6] = a1.z; ax[sl][7] = a1.w;
+    if (meta_lane) {
+#pragma unroll
+      for (int e = 0; e < 3; ++e) apos[sl][e] = ml.accum_pos[(hs * MTPA + min(g, MTPA - 1)) * 3 + e];
+    }
+    bool bad = min(sl ? ng1 : ng0, MTPA) != grid_ng;
+#pragma unroll
+    for (int k = 0; k < kEvIdLoads; ++k) {
+      const int i = tid + k * kUpdThreads;
+      if (i < n4) {
+        int y = (4 * i) / W, xx = (4 * i) % W;
+        const int32_t v[4] = {ids[k].x, ids[k].y, ids[k].z, ids[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bad |= v[e] != (y / p) * cols + xx / p;
+          if (++xx == W) {
+            xx = 0;
+            ++y;
+          }
+        }
+      }
+    }
+    fast = fast && !__syncthreads_or(bad);
+  }
+  if (tid == 0) sh.last = early;
+  __syncthreads();
+  const bool last = uni(sh.last) == a.n_merge - 1;
+  if (last && tid == 0) atomicExch(a.early + static_cast<int64_t>(h) * kArriveStride, 0);
+  if (!fast) {  // update_kernel's merge tile, with its own arrival (same in every workgroup of the head)
+    __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): the ring's copies landed before the tile reuses its LDS
+    __syncthreads();
+    int ticket = 0;
+    upd_merge_wg(a, sh, dyn, h, tile, ticket, 1);
+    upd_finish(a, sh, h, tile, ticket);
+    return;
+  }
+
+  // every load so far complete here, once: the frame loop's waits are then
+  // for the frames in flight only (a wait in the loop for a load from
+  // before it would also wait for every frame issued since)
+  __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0)
+  static_assert(kMaxMergeBlocks < 15, "finalize index in four bits");
+  VeilWords v = vw;
+  uint32_t dec = 0;
+  float wsum[2] = {ws0, ws1};
+  int64_t tpos[2] = {0, 0};
+  bool fresh[2] = {false, false};  // the slot's block began in this call (positions from tpos)
+  uint32_t touched = 0;
+  const int64_t py = (g / cols) * p, px = (g % cols) * p;
+  for (int f0 = 0; f0 < F; f0 += kEfRing) {
+#pragma unroll
+    for (int r = 0; r < kEfRing; ++r) {
+      const int f = f0 + r;
+      if (f >= F) break;
+      const int64_t t = frame_t(f);
+      const float fw = frame_w(f);
+      // frame f's copies complete: the (kEfRing - 1) frames after it may be in flight
+      __builtin_amdgcn_s_waitcnt((((kEfRing - 1) * kTok) & 15) | (7 << 4) | (15 << 8) | ((((kEfRing - 1) * kTok) >> 4) << 14));
+      asm volatile("" ::: "memory");
+      uint4 xr[kTok];
+#pragma unroll
+      for (int m = 0; m < kTok; ++m) xr[m] = ring_read(r, m);
+      VeilStep st;
+      st.d = skip_desc();
+      if (veil) st = veil_decide(v, bf, cap, static_cast<int32_t>(t));
+      veil_advance(v, st);
+      const FrameDesc d = st.d;
+      const int slot = d.accum_slot, is_new = d.is_new_block, fin = d.finalize_idx;
+      const bool merging = d.kind == PKV_DST_MERGE_ACCUM && slot >= 0 && slot < mma;
+      // frame f's step in lane f, for the descriptors: changed (bit 0), slot
+      // (bit 1), new block (bit 2), finalize index + 1 (bits 4..7)
+      if (lane == f && d.kind == PKV_DST_MERGE_ACCUM)
+        dec = 1u | (static_cast<uint32_t>(slot & 1) << 1) | (static_cast<uint32_t>(is_new) << 2) |
+              (static_cast<uint32_t>(fin + 1) << 4);
+      // a completed block enters the record's FIFO (the only step that
+      // changes its arrays; the other words are set from the last step)
+      if (last && wave_s == 0 && fin >= 0) veil_apply_wave(st, rw);
+      auto on_slot = [&](auto sl_c) {
+        constexpr int sl = decltype(sl_c)::value;
+        const int64_t hs = hs0 + sl;
+        if (is_new) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ax[sl][e] = 0.0f;
+          wsum[sl] = 0.0f;
+          tpos[sl] = t;
+          fresh[sl] = true;
+        }
+        touched |= 1u << sl;
+        wsum[sl] = wsum[sl] + fw;
+        if (!own) return;
+        if (g < grid_ng) {
+#pragma unroll
+          for (int m = 0; m < kTok; ++m) {
+            const uint32_t xw[4] = {xr[m].x, xr[m].y, xr[m].z, xr[m].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              ax[sl][2 * e] += fw * bf16_to_f32(static_cast<uint16_t>(xw[e] & 0xffff));
+              ax[sl][2 * e + 1] += fw * bf16_to_f32(static_cast<uint16_t>(xw[e] >> 16));
+            }
+          }
+        }
+        // a block begun here: the group ids of the group's members (one
+        // member per K-side thread), its count and anchor positions
+        if (is_new && !is_v && c < 8 * kTok && g < grid_ng)
+          ml.accum_group_ids[hs * FSEQ + (g / cols) * p * W + (g % cols) * p + (c / 8 / p) * W + (c / 8) % p] = g;
+        if (is_new && meta_lane) {
+          ml.accum_tokens_per_group[hs * MTPA + g] =
+              g < grid_ng ? static_cast<float>(kTok) * static_cast<float>(bf) : 0.0f;
+          if (g < grid_ng) {
+            int64_t *pp = ml.accum_pos + (hs * MTPA + g) * 3;
+            pp[0] = t;
+            pp[1] = py;
+            pp[2] = px;
+          }
+        }
+        if (fin >= 0 && fin < a.MMB && g < grid_ng) {
+          // count * sum(w) for weighted merges, else the reference's count * block_frames
+          const float div = static_cast<float>(kTok) * (a.weights ? wsum[sl] : static_cast<float>(bf));
+          const float inv = div > 0.0f ? 1.0f / div : 0.0f;
+          const int64_t hp = static_cast<int64_t>(h) * a.MMB + fin;
+          uint4 ox;
+          ox.x = pack_bf16x2(ax[sl][0] * inv, ax[sl][1] * inv);
+          ox.y = pack_bf16x2(ax[sl][2] * inv, ax[sl][3] * inv);
+          ox.z = pack_bf16x2(ax[sl][4] * inv, ax[sl][5] * inv);
+          ox.w = pack_bf16x2(ax[sl][6] * inv, ax[sl][7] * inv);
+          st16((is_v ? ml.merge_v : ml.merge_k) + (hp * MTPA + g) * D + c, ox);
+          if (meta_lane) {
+            int64_t *mp = ml.merge_pos + (hp * MTPA + g) * 3;
+            mp[0] = fresh[sl] ? tpos[sl] : apos[sl][0];
+            mp[1] = fresh[sl] ? py : apos[sl][1];
+            mp[2] = fresh[sl] ? px : apos[sl][2];
+          }
+        }
+      };
+      if (merging) {
+        if (slot) on_slot(std::integral_constant<int, 1>());
+        else on_slot(std::integral_constant<int, 0>());
+        if (fin >= 0 && fin < a.MMB && tile == 0 && tid == 0) ml.merge_token_count[static_cast<int64_t>(h) * a.MMB + fin] = grid_ng;
+      }
+      // ring slot r takes frame f + kEfRing (the last frame again past the
+      // end: the same number of copies every frame keeps the waits exact),
+      // once this wave's reads of the slot are complete
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      copy_frame(f + kEfRing, r);
+    }
+  }
+
+  __builtin_amdgcn_s_waitcnt(0xf70);  // vmcnt(0): no copy lands in LDS after the workgroup ends
+  // the slots' sums, once
+  if (own) {
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      if (!(touched & (1u << sl))) continue;
+      float *acc_sum = is_v ? ml.accum_sum_v : ml.accum_sum_k;
+      float4 *ap = reinterpret_cast<float4 *>(acc_sum + ((hs0 + sl) * MTPA + g) * D + c);
+      ap[0] = make_float4(ax[sl][0], ax[sl][1], ax[sl][2], ax[sl][3]);
+      ap[1] = make_float4(ax[sl][4], ax[sl][5], ax[sl][6], ax[sl][7]);
+    }
+  }
+  if (last) {
+    // the record's words after the last step, and the frames' descriptors
+    // (lane f writes frame f's)
+    if (wave_s == 0) {
+      if (lane == kVlCount) rw = (rw & ~0xffu) | (v.count & 0xffu);
+      if (lane == kVlId) rw = static_cast<uint32_t>(v.id0);
+      if (lane == kVlId + 1) rw = static_cast<uint32_t>(v.id1);
+      if (lane == kVlSeen) rw = v.seen0;
+      if (lane == kVlSeen + 1) rw = v.seen1;
+      if (lane == kVlDone) rw = (rw & 0xffff0000u) | (v.done & 0xffffu);
+      if (lane < kVeilWords) reinterpret_cast<uint32_t *>(a.states + h)[kVeilWord0 + lane] = rw;
+      if (lane < F) {
+        FrameDesc fd = skip_desc();
+        if (dec & 1u) {
+          fd.kind = PKV_DST_MERGE_ACCUM;
+          fd.accum_slot = static_cast<int>((dec >> 1) & 1u);
+          fd.is_new_block = static_cast<int>((dec >> 2) & 1u);
+          fd.finalize_idx = static_cast<int>(dec >> 4) - 1;
+          fd.local_idx = static_cast<int32_t>(t_lane) % bf;  // veil_decide's local index
+        }
+        store_desc(a.desc, h * F + lane, lane, h, fd);
+      }
+    }
+    if (tid == 0) {
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        if (!(touched & (1u << sl))) continue;
+        if (fresh[sl]) ml.accum_num_groups[hs0 + sl] = grid_ng;
+        if (ml.accum_weight_sum) ml.accum_weight_sum[hs0 + sl] = wsum[sl];
+      }
+    }
+  }
+}
+
 // Scratch of pkv_merge_accum_static: the per-(head, frame) merge snapshots
 // (MergeWs) in a file-scope device array, for callers that cannot allocate.
 // Each device holds its own copy at its own address; host code never uses
@@ -2291,17 +2675,22 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
   u.n_scat = 0;
   u.n_mh = H;
   u.merge_heads = H >= 64 ? ~uint64_t{0} : (uint64_t{1} << H) - 1;
-  // one frame on a grid of 2 x 2 patches: evict_kernel (which still runs
-  // update_kernel's merge tile for heads its path does not cover)
+  // frames on a grid of 2 x 2 patches: evict_kernel (one frame) or
+  // evict_frames_kernel (several), which still run update_kernel's merge
+  // tile for heads their path does not cover
   auto al16 = [](const void *q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
   const int W = spatial_width;
-  const bool one = F == 1 && MMA <= 2 && W <= FSEQ && FSEQ % W == 0 && W % 2 == 0 && (FSEQ / W) % 2 == 0 &&
-                   FSEQ / 4 <= MTPA && FSEQ <= kEvMaxFseq && D >= 8 * kPreTok && al16(new_k) && al16(new_v) &&
-                   al16(ml->accum_sum_k) && al16(ml->accum_sum_v) && al16(ml->accum_group_ids);
+  const bool grid = MMA <= 2 && W <= FSEQ && FSEQ % W == 0 && W % 2 == 0 && (FSEQ / W) % 2 == 0 &&
+                    FSEQ / 4 <= MTPA && FSEQ <= kEvMaxFseq && D >= 8 * kPreTok && al16(new_k) && al16(new_v) &&
+                    al16(ml->accum_sum_k) && al16(ml->accum_sum_v) && al16(ml->accum_group_ids);
+  const bool one = grid && F == 1, many = grid && F > 1;
   const int gpt = one ? evict_tile_groups(D) : merge_tile_groups(D);
   u.n_merge = (MTPA + gpt - 1) / gpt;
-  const void *kern = one ? reinterpret_cast<const void *>(evict_kernel) : reinterpret_cast<const void *>(update_kernel);
-  const size_t smem = static_cast<size_t>(merge_lds_words(FSEQ, MMA)) * sizeof(int32_t);
+  const void *kern = one ? reinterpret_cast<const void *>(evict_kernel)
+                         : many ? reinterpret_cast<const void *>(evict_frames_kernel)
+                                : reinterpret_cast<const void *>(update_kernel);
+  size_t smem = static_cast<size_t>(merge_lds_words(FSEQ, MMA)) * sizeof(int32_t);
+  if (many) smem = std::max(smem, static_cast<size_t>(kEfRing) * (kUpdThreads / 64) * kPreTok * 1024);
   if (smem > 65536 &&
       hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess)
     return fail(PKV_ERR_HIP, "evict_merge: cannot reserve %zu bytes of LDS", smem);
@@ -2309,6 +2698,12 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
     hipLaunchKernelGGL(evict_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u.states,
                        u.t_vals, u.weights, u.ml.accum_num_groups, u.ml.accum_weight_sum, u.n_merge, u.MMA, u);
     return check_launch("evict_kernel");
+  }
+  if (many) {
+    hipLaunchKernelGGL(evict_frames_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream),
+                       u.states, u.t_vals, u.weights, u.ml.accum_num_groups, u.ml.accum_weight_sum, u.n_merge, u.MMA,
+                       u);
+    return check_launch("evict_frames_kernel");
   }
   hipLaunchKernelGGL(update_kernel, dim3(H * u.n_merge), dim3(kUpdThreads), smem, as_stream(stream), u);
   return check_launch("update_kernel");

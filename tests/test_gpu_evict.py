@@ -138,3 +138,60 @@ def test_evict_one_frame_head_dim_64():
     # head_dim 64: 8 chunks per group row, twice the groups per workgroup
     calls = [[int(t)] for t in np.random.default_rng(12).integers(0, 20, 24)]
     _evict_run(H=3, FSEQ=1560, W=52, calls=calls, seed=12, weighted=True, D=64)
+
+
+# ---- several frames per call (evict_frames_kernel on the regular grid) ------
+
+def _grouped(ts, F):
+    return [list(map(int, ts[i:i + F])) for i in range(0, len(ts), F)]
+
+
+@pytest.mark.parametrize("F,weighted", [(5, False), (7, True), (8, True)])
+def test_evict_frames_out_of_order_and_repeated(F, weighted):
+    # calls of F frames in random order with repeats: blocks begun while both
+    # slots are busy (slot 0 evicted), repeated frames, FIFO shifts at
+    # capacities 2 and 3, and calls that open with both slots holding blocks
+    rng = np.random.default_rng(41 + F)
+    recs = [O.make_merge(2, 2), O.make_merge(2, 3), O.make_merge(2, 6)]
+    _evict_run(H=3, FSEQ=1560, W=52, calls=_grouped(rng.integers(0, 28, 6 * F), F), seed=15, weighted=weighted,
+               recs=recs)
+
+
+def test_evict_frames_mixed_kinds_and_patch_sizes():
+    # heads the several-frame path does not cover (Wave, patch-1 Veil, Anchor)
+    # beside patch-2 Veil heads in every launch
+    recs = [O.make_merge(2, 4), O.make_cyclic(4, 2), O.make_merge(1, 3), O.make_stride(2, 3), O.make_merge(2, 2)]
+    _evict_run(H=5, FSEQ=1560, W=52, calls=_grouped(np.arange(24), 4), seed=16, weighted=True, recs=recs)
+
+
+@pytest.mark.parametrize("how", ["permuted", "swapped_pair"])
+def test_evict_frames_continue_block_by_its_stored_group_ids(how):
+    # stored ids rewritten between calls: a call whose first frames continue
+    # such a block runs the general tile for the head
+    def tamper(ci, acc, dacc):
+        if ci != 1:
+            return
+        gid = acc["gid"]
+        rng = np.random.default_rng(19)
+        for h in range(gid.shape[0]):
+            for s in range(gid.shape[1]):
+                if how == "permuted":
+                    gid[h, s] = gid[h, s][rng.permutation(gid.shape[2])]
+                else:
+                    gid[h, s, 0], gid[h, s, 60] = gid[h, s, 60].copy(), gid[h, s, 0].copy()
+        dacc["gid"].copy_(to_dev(gid))
+    _evict_run(H=2, FSEQ=1560, W=52, calls=_grouped(np.arange(1, 16), 3), seed=17, weighted=True, tamper=tamper)
+
+
+def test_evict_frames_head_dim_64():
+    calls = _grouped(np.random.default_rng(18).integers(0, 20, 30), 5)
+    _evict_run(H=3, FSEQ=1560, W=52, calls=calls, seed=18, weighted=True, D=64)
+
+
+@pytest.mark.parametrize("F", [40, 64])
+def test_evict_frames_long_calls(F):
+    # the config-4 step as one call (40 frames), and the most frames a call
+    # takes; a second call continues the blocks the first left open
+    calls = [list(range(1, F + 1)), list(range(F + 1, F + 7))]
+    recs = [O.make_merge(2, 6), O.make_merge(2, 2)]
+    _evict_run(H=2, FSEQ=1560, W=52, calls=calls, seed=20 + F, weighted=True, recs=recs)

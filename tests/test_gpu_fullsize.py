@@ -203,6 +203,7 @@ def test_config4_weighted_evictions():
     desc1 = [torch.full((H,), -1, dtype=torch.int32, device=DEV) for _ in range(8)]
     tok = np.arange(FSEQ)
     ws = torch.zeros(ops.mega_evict_merge_workspace_size(H), dtype=torch.uint8, device=DEV)
+    frames_k, frames_v, weights, want_desc = [], [], [], []
     for e in range(E):
         k = O.f32_to_bf16(rng.standard_normal((1, H, FSEQ, D)).astype(np.float32))
         v = O.f32_to_bf16(rng.standard_normal((1, H, FSEQ, D)).astype(np.float32))
@@ -213,6 +214,10 @@ def test_config4_weighted_evictions():
         w = rng.uniform(0.1, 1.0, 1).astype(np.float32)
         d_ = O.state_update(states, [e + 1], 1)
         O.merge_accum(states, k, v, pos, d_, acc, weights=w)
+        frames_k.append(k)
+        frames_v.append(v)
+        weights.append(w)
+        want_desc.append(d_.copy())
         ops.mega_state_update(sd, torch.tensor([e + 1], dtype=torch.int64, device=DEV), *desc, H, 1, 1)
         ops.mega_merge_accum_weighted(sd, to_dev(k).view(torch.bfloat16), to_dev(v).view(torch.bfloat16), to_dev(pos),
                                       desc[0], desc[4], desc[6], desc[7], to_dev(w), dacc["sum_k"], dacc["sum_v"],
@@ -222,13 +227,28 @@ def test_config4_weighted_evictions():
                              to_dev(v).view(torch.bfloat16), 52, to_dev(w), *desc1, dacc1["sum_k"], dacc1["sum_v"],
                              dacc1["pos"], dacc1["gid"], dacc1["tpg"], dacc1["ng"], dacc1["wsum"], dacc1["mk"],
                              dacc1["mv"], dacc1["mpos"], dacc1["mtc"], ws)
+    # all 40 evictions as one call of 40 frames (the several-frame kernel)
+    sd40 = to_dev(O.states_to_bytes([O.make_merge(2, 6) for _ in range(H)]).view(np.uint8).reshape(-1).copy())
+    dacc40 = {n: to_dev(np.zeros_like(a)) for n, a in acc.items()}
+    desc40 = [torch.full((H * E,), -7, dtype=torch.int32, device=DEV) for _ in range(8)]
+    ops.mega_evict_merge(sd40, torch.arange(1, E + 1, dtype=torch.int64, device=DEV),
+                         to_dev(np.concatenate(frames_k)).view(torch.bfloat16),
+                         to_dev(np.concatenate(frames_v)).view(torch.bfloat16), 52, to_dev(np.concatenate(weights)),
+                         *desc40, dacc40["sum_k"], dacc40["sum_v"], dacc40["pos"], dacc40["gid"], dacc40["tpg"],
+                         dacc40["ng"], dacc40["wsum"], dacc40["mk"], dacc40["mv"], dacc40["mpos"], dacc40["mtc"], ws)
     torch.cuda.synchronize()
     assert np.array_equal(to_np(sd), states)
     assert np.array_equal(to_np(sd1), states), "mega_evict_merge: state records differ"
+    assert np.array_equal(to_np(sd40), states), "mega_evict_merge, 40 frames: state records differ"
+    for i in range(8):
+        want = np.stack([want_desc[e][i] for e in range(E)], axis=1).reshape(-1)  # index h * E + e
+        if i == 2:  # src_frame: the frame's index within the call
+            want = np.tile(np.arange(E), H)
+        assert np.array_equal(to_np(desc40[i]), want.astype(np.int32)), f"40 frames: descriptor array {i} differs"
     for i in range(8):
         assert torch.equal(desc[i], desc1[i]), f"mega_evict_merge: descriptor array {i} differs"
     for n, a in acc.items():
-        for tag, dd in (("two ops", dacc), ("mega_evict_merge", dacc1)):
+        for tag, dd in (("two ops", dacc), ("mega_evict_merge", dacc1), ("mega_evict_merge, 40 frames", dacc40)):
             got = to_np(dd[n])
             assert np.array_equal(got.view(a.dtype) if got.dtype != a.dtype else got, a), f"{tag}: {n} differs"
 
