@@ -14,10 +14,12 @@
   oracle's state machine and planner.  For three layers chosen to cover the
   label mixes, the oracle MegaCache model runs the whole rollout on the same
   data: pools and the packed K / V / positions bit-exact.
+  Then the production pass pattern at full size on those three layers:
+  chunks of 4 noisy passes and a clean pass, checked after every pass.
 * Config 4: 40 single-frame weighted Veil evictions of 12 heads, through the
-  reference's two ops and through the one-launch mega_evict_merge, both
-  bit-exact against the oracle (anchors, positions, counts and the fp32
-  accumulators).
+  reference's two ops, through the one-launch mega_evict_merge and as one
+  call of 40 frames, all bit-exact against the oracle (anchors, positions,
+  counts and the fp32 accumulators).
 * Config 5: the causal DiT rollout in the Wan2.1-T2V-1.3B shape for 8
   chunks: finite outputs, and the caches advanced as the policy dictates
   (state records against the oracle state machine, valid counts and merge
@@ -179,6 +181,101 @@ def test_config3_full_step40():
                     ("merge_pos", mgr.merge_pos_pool())]:
         for l in watch:
             assert np.array_equal(to_np(t[l]), getattr(ref, name)[l]), f"layer {l}: pool {name} differs"
+
+
+def test_config3_noisy_clean_chunks():
+    """Full size, shipped policy, on the three layers config 3 watches (as a
+    cache of three layers): 6 chunks of 3 frames, each run as the pipeline
+    runs it -- 4 noisy passes, then the clean pass (causal_inference.py:
+    445-502) -- so that the recent FIFO shifts once per block, evicted frames
+    reach the middle and merge pools, and noisy passes read the committed
+    baseline.  After every pass: pools, valid and merge counts, state
+    records and the Veil accumulators bit-exact against MegaCacheRef; for
+    every noisy pass the plan and the packed K / V / positions bit-exact,
+    and for each chunk's first noisy pass the attention on 64 sampled query
+    rows of every (frame, head) within the north star's tolerance of
+    float64."""
+    from pyramidkv import factory
+    from pyramidkv._mega_cache import build_mega_caches
+    from pyramidkv.rope import wan_freqs
+    F, chunks, noisy = 3, 6, 4
+    labels_all = factory.load_head_labels(factory.SHIPPED_LABELS_CSV, L, H)
+    watch = _oracle_layers(labels_all)
+    Lw = len(watch)
+    comps = factory.shipped_compositions(Lw, H, labels=[list(labels_all[l]) for l in watch])
+    caches = build_mega_caches(Lw, H, D, FSEQ, 3, 24, 4, comps, max_attend_chunks=8, device=DEV,
+                               freqs=wan_freqs(D), spatial_width=52, spatial_height=30,
+                               **factory.PYRAMID_FORCING_REMAP)
+    ctx = caches[0].ctx
+    mgr = ctx.mgr
+    tables = O.rope_tables(D)
+    ctx.freq_parts_flat = tuple(to_dev(t) for t in tables)
+    geo = O.Geometry(Lw, H, D, FSEQ, 3, 24, 4, max_attend_chunks=8)
+    ref = O.MegaCacheRef(geo, to_np(ctx.states_bytes).reshape(Lw, -1), to_np(ctx.sink_caps_per_head).reshape(Lw, H),
+                         spatial_width=52, sink_mode=1, cmin=18, cmax=21, lag=0, tables=tables)
+    print(f"config 3 noisy/clean: layers {watch} of the shipped policy, {chunks} chunks x ({noisy} noisy + 1 clean)",
+          flush=True)
+    pools = [("sink_k", mgr.sink_k_pool), ("sink_v", mgr.sink_v_pool), ("sink_pos", mgr.sink_pos_pool),
+             ("middle_k", mgr.middle_k_pool), ("middle_v", mgr.middle_v_pool), ("middle_pos", mgr.middle_pos_pool),
+             ("recent_k", mgr.recent_k_pool), ("recent_v", mgr.recent_v_pool), ("recent_pos", mgr.recent_pos_pool),
+             ("merge_k", mgr.merge_k_pool), ("merge_v", mgr.merge_v_pool), ("merge_pos", mgr.merge_pos_pool),
+             ("merge_token_count", mgr.merge_token_count), ("valid_count", mgr.valid_count)]
+    accs = [("sum_k", mgr.merge_accum_sum_k), ("sum_v", mgr.merge_accum_sum_v), ("pos", mgr.merge_accum_pos),
+            ("gid", mgr.merge_accum_group_ids), ("tpg", mgr.merge_accum_tokens_per_group),
+            ("ng", mgr.merge_accum_num_groups), ("wsum", mgr.merge_accum_weight_sum)]
+    rng = np.random.default_rng(33)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(33)
+    for c in range(chunks):
+        start = c * F * FSEQ
+        for p in range(noisy + 1):
+            mode = "clean" if p == noisy else "noisy"
+            where = f"chunk {c} pass {p} ({mode})"
+            for l in range(Lw):
+                kd = torch.randn(1, F * FSEQ, H, D, generator=gen, device=DEV).to(torch.bfloat16)
+                vd = torch.randn(1, F * FSEQ, H, D, generator=gen, device=DEV).to(torch.bfloat16)
+                caches[l].update(kd, vd, start, cache_update_mode=mode)
+                ref.update(l, to_np(kd).reshape(F * FSEQ, H, D), to_np(vd).reshape(F * FSEQ, H, D), start, mode)
+                if mode != "noisy":
+                    continue
+                want = ref.plan_pack(l, start, F)
+                cu = caches[l].attend_kv(start, F)
+                n_pairs, total = F * H, want["total"]
+                assert np.array_equal(to_np(cu), want["cu"][:n_pairs + 1]), f"{where} layer {l}: cu_seqlens_k"
+                assert np.array_equal(to_np(mgr.k_flat_out()).reshape(-1, D)[:total], want["k"]), f"{where}: K"
+                assert np.array_equal(to_np(mgr.v_flat_out()).reshape(-1, D)[:total], want["v"]), f"{where}: V"
+                assert np.array_equal(to_np(mgr.pos_flat_out())[:total], want["pos"]), f"{where}: pos"
+                if p != 0:
+                    continue
+                q = torch.randn(1, F * FSEQ, H, D, generator=gen, device=DEV).to(torch.bfloat16)
+                out = caches[l].attend(q, start)[0].float().cpu().numpy().astype(np.float64)
+                qf = q[0].float().cpu().numpy().astype(np.float64)
+                kf = O.bf16_to_f32(want["k"]).astype(np.float64)
+                vf = O.bf16_to_f32(want["v"]).astype(np.float64)
+                errs = []
+                for f in range(F):
+                    rows = f * FSEQ + rng.choice(FSEQ, 64, replace=False)
+                    for h in range(H):
+                        lo, hi = want["cu"][f * H + h], want["cu"][f * H + h + 1]
+                        sc = qf[rows, h] @ kf[lo:hi].T * D ** -0.5
+                        pr = np.exp(sc - sc.max(axis=1, keepdims=True))
+                        pr /= pr.sum(axis=1, keepdims=True)
+                        errs.append(np.abs(out[rows, h] - pr @ vf[lo:hi]))
+                err = np.concatenate(errs)
+                assert err.max() < 2e-2 and err.mean() < 2e-3, f"{where} layer {l}: attention {err.max()} {err.mean()}"
+            torch.cuda.synchronize()
+            for name, fn in pools:
+                want = getattr(ref, name)
+                got = to_np(fn()).reshape(want.shape)
+                if not np.array_equal(got, want):
+                    bad = np.argwhere(got != want)
+                    raise AssertionError(f"{where}: {name} differs at {len(bad)} places, first {bad[:4].tolist()}")
+            assert np.array_equal(to_np(ctx.states_bytes).reshape(ref.states.shape), ref.states), f"{where}: records"
+            for name, fn in accs:
+                got = to_np(fn())
+                for l in range(Lw):
+                    w = ref.acc[l][name]
+                    assert np.array_equal(got[l].reshape(w.shape), w), f"{where}: accumulator {name} of layer {l}"
 
 
 def test_config4_weighted_evictions():
