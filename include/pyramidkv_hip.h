@@ -331,6 +331,11 @@ typedef struct pkv_attn_args {
   int32_t causal; /* must be 0 */
 } pkv_attn_args;
 
+/* Launches of head_dim 128 with at least 1,024 query tiles of 384 rows run
+ * one workgroup per compute unit, claiming tiles from counters in a static
+ * device array: one 128-byte block per stream, taken on the stream's first
+ * such launch (launches on different streams may overlap); past 64 streams
+ * on a device they run one tile per workgroup.  Nothing is allocated. */
 int pkv_ragged_attn_fwd(const pkv_attn_args *args, pkv_stream_t stream);
 
 /* The same attention with a device workspace (replaces the same call,
@@ -382,7 +387,9 @@ typedef struct pkv_update_args {
  * at the grid positions (t_vals[f], tok / W, tok % W) -- the positions
  * MegaCache.update gives its frames (_mega_cache.py:203-215) -- with
  * optional frame weights.  Results equal the two calls in sequence on those
- * positions; new_k/new_v are [F, H, FSEQ, D] bf16.  It has no counterpart
+ * positions; new_k/new_v are [F, H, FSEQ, D] bf16, 1 <= F <= 64 (several
+ * frames per call read each frame once and keep the fp32 sums on chip; the
+ * results equal F one-frame calls bit for bit).  It has no counterpart
  * in the reference, which evicts through mega_state_update
  * (anchor_store_update.cu:257-269) and mega_merge_accum
  * (mega_merge_accum.cu:52-340); it is for callers that evict frames
