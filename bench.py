@@ -983,6 +983,7 @@ def secondary(args):
     out["config4_veil_merge"] = {
         "value": round(gbs4, 2), "unit": "GB/s", "ms_per_step": round(c4["ms"], 4), "timing": "hip_graph_replay",
         "evictions_per_step": EVICTIONS, "frames_per_call": EVICTIONS, "bytes_per_step": c4["bytes"],
+        "evictions_per_s": round(EVICTIONS / (c4["ms"] * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs4, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs4 / PEAK_HBM_GBS, 4), "traffic": None,
                      "dominant_kernel": "evict_frames_kernel",
@@ -990,6 +991,7 @@ def secondary(args):
         "parity_bit_exact": c4["parity"], "graph_replay_matches_eager": c4["graph_same"], "cpu_baseline": c4["cpu"],
         "single_frame_calls": {
             "frames_per_call": 1, "ms_per_step": round(c4s["ms"], 4), "bytes_per_step": c4s["bytes"],
+            "evictions_per_s": round(EVICTIONS / (c4s["ms"] * 1e-3), 1),
             "value": round(gbs4s, 2), "unit": "GB/s", "frac": round(gbs4s / PEAK_HBM_GBS, 4),
             "dominant_kernel": "evict_kernel", "dominant_kernel_traffic": traffic_bytes("evict_kernel"),
             "parity_bit_exact": c4s["parity"], "graph_replay_matches_eager": c4s["graph_same"]}}
