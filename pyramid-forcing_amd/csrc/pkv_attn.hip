@@ -2112,16 +2112,20 @@ static int *queue_for(hipStream_t st) {
   static int used[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  // the array's address on this device (the host-side name is not one),
+  // looked up on every call: after a device reset the array is a new one,
+  // and every block of it is taken afresh
+  void *ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_attn_queue)) != hipSuccess || !ptr) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
+  if (base[dev] != static_cast<int *>(ptr)) {
+    for (auto it = blocks.begin(); it != blocks.end();) it = it->first.first == dev ? blocks.erase(it) : std::next(it);
+    base[dev] = static_cast<int *>(ptr);
+    used[dev] = 0;
+  }
   const auto key = std::make_pair(dev, st);
   const auto found = blocks.find(key);
   if (found != blocks.end()) return found->second;
-  if (!base[dev]) {
-    // the array's address on this device (the host-side name is not one)
-    void *ptr = nullptr;
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_attn_queue)) != hipSuccess || !ptr) return nullptr;
-    base[dev] = static_cast<int *>(ptr);
-  }
   if (used[dev] >= kQueueSlots) return nullptr;
   int *q = base[dev] + used[dev] * kQueueInts;
   hipLaunchKernelGGL(queue_clear_kernel, dim3(1), dim3(64), 0, st, q);

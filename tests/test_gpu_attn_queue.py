@@ -100,3 +100,26 @@ def test_queue_launches_on_two_streams_at_once():
         assert np.array_equal(to_np(o), alone[i % 2]), f"launch {i} on stream {i % 2} differs from its launch alone"
     c = cases[1][3]
     _check(alone[1], c[0], c[1], c[2], c[3], c[4], H)
+
+
+def test_queue_launches_beyond_the_counter_blocks():
+    """70 streams, one launch each: the first 64 streams of the process on
+    this device (fewer, if earlier tests took some) get counter blocks, the
+    rest run one tile per workgroup; every launch equals the default
+    stream's bit for bit."""
+    rng = np.random.default_rng(79)
+    H = 12
+    Lq, Lk = _mixed(rng, H=H)
+    q, k, v, cu_q, cu_k = _case(rng, Lq, Lk, H)
+    B, max_q = len(Lq), int(Lq.max())
+    dev_case = (to_dev(q), to_dev(k), to_dev(v), to_dev(cu_q), to_dev(cu_k))
+    want = to_np(_launch(dev_case, B, H, max_q))
+    streams = [torch.cuda.Stream(device=DEV) for _ in range(70)]
+    outs = []
+    torch.cuda.synchronize()
+    for st in streams:
+        with torch.cuda.stream(st):
+            outs.append(_launch(dev_case, B, H, max_q))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert np.array_equal(to_np(o), want), f"stream {i} differs"
