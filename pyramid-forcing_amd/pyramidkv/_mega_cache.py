@@ -71,6 +71,9 @@ class MegaCacheCtx:
     freq_parts_flat: tuple = None
     # per layer: (t0, frames) of the block whose recent shift is in the pool but not committed
     pending_block: list = field(default_factory=list)
+    # per layer: the committed recent FIFO (K, V, positions), copied at a block's first noisy pass
+    # (allocated on first use); restored when a pass for another block comes before the commit
+    recent_backup: dict = field(default_factory=dict)
     cu_q: dict = field(default_factory=dict)
     # key-split attention for attend (off by default: on a rollout's per-layer
     # launches it measured no faster than the unsplit kernels) and the
@@ -114,11 +117,15 @@ class MegaCache:
             ctx.committed_vc = ctx.mgr.valid_count().clone()
         block = (t0, L_in // FSEQ)
         pending = ctx.pending_block[l]
-        if pending is not None and pending != block:
-            raise RuntimeError(
-                f"MegaCache.update: layer {l} has an uncommitted noisy pass for block t={pending[0]} of "
-                f"{pending[1]} frames; commit it with a clean pass before updating block t={t0} of {block[1]} frames")
         clean = cache_update_mode == "clean"
+        if pending is not None and pending != block:
+            # another block's noisy pass is in the recent FIFO, uncommitted: back to the committed FIFO, as
+            # the reference's restore of its snapshot (_mega_cache.py:226-245); this pass then shifts afresh
+            self._recent_fifo(restore=True)  # (the backup still holds the committed FIFO)
+        elif pending is None and not clean:
+            self._recent_fifo(restore=False)  # a block's first noisy pass: keep the committed FIFO
+        if pending != block:
+            pending = None
         nk = new_k if new_k.dtype == torch.bfloat16 else new_k.to(torch.bfloat16)
         nv = new_v if new_v.dtype == torch.bfloat16 else new_v.to(torch.bfloat16)
         if nk.stride(-1) != 1 or nk.stride(-2) != D:
@@ -130,6 +137,23 @@ class MegaCache:
                                 l, t0, 1 if clean else 0, 1 if pending == block else 0, ctx.spatial_width,
                                 ctx.layer_merge_heads[l])
         ctx.pending_block[l] = None if clean else block
+
+    def _recent_fifo(self, restore: bool) -> None:
+        """Copy this layer's recent K / V / positions into the layer's backup
+        (restore=False), or back from it (restore=True)."""
+        ctx, l = self.ctx, self.layer_idx
+        mgr = ctx.mgr
+        pools = (mgr.recent_k_pool()[l], mgr.recent_v_pool()[l], mgr.recent_pos_pool()[l])
+        backup = ctx.recent_backup.get(l)
+        if restore:
+            for dst, src in zip(pools, backup):
+                dst.copy_(src)
+            return
+        if backup is None:
+            backup = tuple(torch.empty_like(t) for t in pools)
+            ctx.recent_backup[l] = backup
+        for dst, src in zip(backup, pools):
+            dst.copy_(src)
 
     def last_update_descriptors(self, frames: int):
         """The 8 state-machine descriptor arrays of the last update call."""

@@ -191,15 +191,37 @@ def test_megacache_continues_block_by_its_stored_group_ids(how):
     assert int(to_np(mgr.merge_token_count())[0, 0].max()) > 0, "block 0 was finalized"
 
 
-def test_megacache_rejects_update_of_new_block_while_noisy_pending():
-    L, H, D, FS, W = 1, 2, 64, 16, 4
-    caches, _ref, _g = _build(L, H, D, FS, W, [[-1, 1]], chunks=2)
-    k = torch.zeros(1, FS, H, D, dtype=torch.bfloat16, device=DEV)
-    caches[0].update(k, k, 0, cache_update_mode="noisy")
-    with pytest.raises(RuntimeError, match="uncommitted noisy pass"):
-        caches[0].update(k, k, FS, cache_update_mode="noisy")
-    caches[0].update(k, k, 0, cache_update_mode="clean")
-    caches[0].update(k, k, FS, cache_update_mode="noisy")
+@pytest.mark.parametrize("FS,W", [(64, 8), (63, 9)])
+def test_megacache_pass_for_another_block_before_the_commit(FS, W):
+    """Noisy passes for a block, then a pass for another block before the
+    first block's clean pass -- another t0, or the same t0 with another frame
+    count -- as the reference allows (it restores its committed snapshot
+    first, _mega_cache.py:226-245): pools, counters, records, accumulators,
+    plan and packed K/V/pos bit-exact against the oracle after every pass,
+    which restores the committed recent FIFO on every update."""
+    rng = np.random.default_rng(11)
+    L, H, D = 2, 6, 128
+    labels = [[-1, 1, 2, -1, 1, 2], [2, -1, 1, 1, 2, -1]]
+    caches, ref, g = _build(L, H, D, FS, W, labels, chunks=4)
+    # (t0, frames, mode): blocks of 3 frames committed until the recent window
+    # shifts, then abandoned noisy passes of other blocks between the passes
+    passes = [(0, 3, "clean"), (3, 3, "clean"),
+              (6, 3, "noisy"), (6, 3, "noisy"), (9, 3, "noisy"), (9, 3, "clean"),
+              (12, 3, "noisy"), (12, 2, "noisy"), (12, 2, "clean"),
+              (14, 3, "noisy"), (17, 1, "clean"), (18, 3, "noisy"), (18, 3, "noisy"), (18, 3, "clean")]
+    for pi, (t0, F, mode) in enumerate(passes):
+        print(f"pass {pi}: t0={t0} F={F} {mode} FS={FS}", flush=True)
+        for layer in range(L):
+            k = _rand_bf16(rng, F * FS, H, D)
+            v = _rand_bf16(rng, F * FS, H, D)
+            kd = to_dev(k).view(torch.bfloat16).view(1, F * FS, H, D)
+            vd = to_dev(v).view(torch.bfloat16).view(1, F * FS, H, D)
+            caches[layer].update(kd, vd, t0 * FS, cache_update_mode=mode)
+            ref.update(layer, k, v, t0 * FS, mode)
+            q = _rand_bf16(rng, F * FS, H, D)
+            _compare_attend(caches[layer], ref, layer, t0 * FS, F, q, f"pass {pi} layer {layer}")
+        torch.cuda.synchronize()
+        _compare_pools(caches, ref, f"pass {pi} (t0={t0}, F={F}, {mode})")
 
 
 def test_megacache_modes_other_than_noisy_clean_are_noops():

@@ -214,11 +214,13 @@ def test_meta_dispatch_shapes():
     assert tuple(kr.shape) == (1000, 128)
 
 
-def test_megacache_rejects_a_second_block_while_a_noisy_pass_is_pending():
-    """The recent-window shift of a noisy pass stays in the pool until the
-    block's clean pass; an update for another block -- another t0, or the
-    same t0 with another frame count (whose shift differs) -- is refused
-    before anything is launched, and the pending marker is kept."""
+def test_megacache_keeps_and_restores_the_committed_recent_fifo():
+    """A block's first noisy pass copies the layer's recent FIFO (the
+    committed one: the last pass was clean) into the layer's backup; a pass
+    for another block while a noisy pass is pending -- another t0, or the
+    same t0 with another frame count (whose shift differs) -- first copies
+    it back, as the reference restores its snapshot (_mega_cache.py:226-245).
+    Both happen before the launch, which a CPU manager then refuses."""
     from pyramidkv import _ops
     if not _ops.available():
         pytest.skip("torch binding not built")
@@ -229,10 +231,21 @@ def test_megacache_rejects_a_second_block_while_a_noisy_pass_is_pending():
     comps = [[HeadComposition(f"h{h}", 0, sink_frames=1, recent_frames=3) for h in range(H)]]
     cache = build_mega_caches(1, H, D, FS, 1, 1, 3, comps, max_attend_chunks=1, device="cpu", spatial_width=4,
                               spatial_height=2, **factory.PYRAMID_FORCING_REMAP)[0]
+    mgr = cache.ctx.mgr
+    pools = lambda: (mgr.recent_k_pool()[0], mgr.recent_v_pool()[0], mgr.recent_pos_pool()[0])
     kv = lambda F: torch.zeros(1, F * FS, H, D, dtype=torch.bfloat16)
-    cache.ctx.pending_block[0] = (5, 3)  # a noisy pass of block t=5 (3 frames) is in the pool
-    with pytest.raises(RuntimeError, match="uncommitted noisy pass for block t=5 of 3 frames"):
-        cache.update(kv(3), kv(3), 8 * FS, cache_update_mode="noisy")
-    with pytest.raises(RuntimeError, match="block t=5 of 2 frames"):
-        cache.update(kv(2), kv(2), 5 * FS, cache_update_mode="clean")
-    assert cache.ctx.pending_block[0] == (5, 3)
+    for i, t in enumerate(pools()):
+        t.fill_(i + 1)
+    with pytest.raises(Exception):  # the launch: no CPU kernel
+        cache.update(kv(3), kv(3), 5 * FS, cache_update_mode="noisy")
+    backup = cache.ctx.recent_backup[0]
+    assert all(torch.equal(b, t) for b, t in zip(backup, pools()))
+    for t in pools():
+        t.fill_(9)  # as if the pending pass had shifted and written the FIFO
+    cache.ctx.pending_block[0] = (5, 3)
+    for start, F in ((8 * FS, 3), (5 * FS, 2)):
+        with pytest.raises(Exception):
+            cache.update(kv(F), kv(F), start, cache_update_mode="noisy" if F == 3 else "clean")
+        assert all(int(t.min()) == int(t.max()) == i + 1 for i, t in enumerate(pools())), (start, F)
+        for t in pools():
+            t.fill_(9)
