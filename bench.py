@@ -8,10 +8,12 @@ BASELINE workload "config 2": 30 layers x 12 heads, head_dim 128, bf16,
 1,560 tokens; capped at 21 frames).  One step = one launch of the ragged
 attention kernel over all 360 (layer, head) sequences, inputs resident in
 HBM.  The "secondary" object reports config 1 (the single-layer step:
-update, plan + pack with RoPE, query RoPE, attention), config 3 (30-layer
-cache update + plan + pack at step 40, HBM GB/s), config 4 (Veil merge
-accumulate, HBM GB/s) and config 5 (the causal DiT rollout), each with a
-check against the CPU oracle and the oracle's own throughput as the CPU
+update, plan + pack with RoPE, query RoPE, attention), config 2 with spiked
+rows (the softmax's rebase and slow-pass costs), config 3 (30-layer cache
+update + plan + pack at step 40, HBM GB/s), config 4 (Veil merge
+accumulate of 40 evictions as one 40-frame call, HBM GB/s, with the 40
+one-frame calls beside it) and config 5 (the causal DiT rollout), each with
+a check against the CPU oracle and the oracle's own throughput as the CPU
 baseline where the config has one.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
