@@ -212,7 +212,11 @@ class CausalDiT:
             # feed-forward
             xn2 = ops.dit_residual_layer_norm_(x, self._mm(yc.view(N, s.dim), blk["co"]), None, mod[4], mod[3], True,
                                                eps)
-            h = ops.dit_gelu_tanh(self._mm(xn2, blk["ffn1"]))
+            # FFN up-projection with the bias and tanh-GELU in the GEMM's
+            # epilogue (applied to the fp32 product before the bf16 rounding;
+            # 147-150 against 158-173 us for the GEMM and dit_gelu_tanh)
+            w1, b1 = blk["ffn1"]
+            h = torch._addmm_activation(b1, xn2.to(torch.bfloat16), w1.t(), use_gelu=True)
             nxt = mods[bi + 1] if bi + 1 < len(self.blocks) else hm
             xn = ops.dit_residual_layer_norm_(x, self._mm(h, blk["ffn2"]), mod[5], nxt[1], nxt[0], True, eps)
         out = self._mm(xn, self.w_head)
