@@ -799,7 +799,7 @@ def bench_merge(steps: int, warmup: int, seed: int = 0, frames_per_call: int = E
 E2E_CHUNKS = 80  # 240 latent frames in chunks of 3 (about 60 s of video)
 
 
-def bench_e2e(chunks: int = E2E_CHUNKS, seed: int = 0):
+def bench_e2e(chunks: int = E2E_CHUNKS, seed: int = 0, tune_gemms: bool = False):
     """Config 5: the causal DiT rollout in the Wan2.1-T2V-1.3B shape with
     random weights, cross-attention to a random 512 x 4096 text context, the
     pyramid cache of a seeded 30 x 12 label matrix, 4 noisy denoising
@@ -812,9 +812,19 @@ def bench_e2e(chunks: int = E2E_CHUNKS, seed: int = 0):
 
     from pyramidkv import factory
     from pyramidkv._mega_cache import build_mega_caches
-    from pyramidkv.causal_dit import CausalDiT, WanShape, rollout
+    from pyramidkv.causal_dit import GEMM_TUNING_FILE, CausalDiT, WanShape, rollout, use_tuned_gemms
     from pyramidkv.rope import wan_freqs
 
+    if tune_gemms:  # TunableOp tries the GEMM solutions of every shape the rollout runs and writes the file
+        import torch.cuda.tunable as tunable
+        tunable.enable(True)
+        tunable.tuning_enable(True)
+        tunable.set_max_tuning_duration(30)
+        tunable.set_max_tuning_iterations(50)
+        tunable.set_filename(GEMM_TUNING_FILE)
+        tuned = False
+    else:
+        tuned = use_tuned_gemms()
     shape = WanShape()
     dev = "cuda:0"
     model = CausalDiT(shape, dev, seed=seed)
@@ -833,7 +843,8 @@ def bench_e2e(chunks: int = E2E_CHUNKS, seed: int = 0):
             "pyramid_path_ms_per_chunk": round(r["cache_ms"] / r["chunks"], 2),
             "pyramid_path_share": round(r["cache_ms"] / r["ms"], 4),
             "model": "random-init Wan2.1-T2V-1.3B shape (30 blocks, dim 1536, 12 heads, FFN 8960)",
-            "labels": "seeded 30x12 over {-1,1,2}", "text_context": "random 512x4096"}
+            "labels": "seeded 30x12 over {-1,1,2}", "text_context": "random 512x4096",
+            "gemm_solutions": "TunableOp file " + os.path.basename(GEMM_TUNING_FILE) if tuned else "torch default"}
 
 
 def main():
@@ -844,6 +855,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true", help="skip the config-3 / 4 / 5 measurements")
     ap.add_argument("--e2e-chunks", type=int, default=E2E_CHUNKS, help="3-frame chunks of the config-5 rollout")
+    ap.add_argument("--tune-gemms", action="store_true",
+                    help="run two chunks of the config-5 rollout with torch TunableOp tuning on and write the GEMM "
+                         "solutions to pyramid-forcing_amd/pyramidkv/gemm_tuning_gfx950.csv")
     ap.add_argument("--workload", choices=["all", "attn", "config1", "cache", "merge", "e2e", "copy"], default="all",
                     help="run one workload alone and print its timing (for profiler runs)")
     args = ap.parse_args()
@@ -853,6 +867,10 @@ def main():
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if args.tune_gemms:
+        r = bench_e2e(2, tune_gemms=True)
+        print(json.dumps({"tuned_gemms": True, "ms_per_chunk_while_tuning": r["ms_per_chunk"]}))
+        return
     if args.workload != "all":
         print(json.dumps(single_workload(args)))
         return

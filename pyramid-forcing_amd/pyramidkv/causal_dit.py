@@ -29,6 +29,7 @@ of throughput, not of sample quality.
 from __future__ import annotations
 
 import math
+import os
 from dataclasses import dataclass
 
 import torch
@@ -36,6 +37,26 @@ import torch.nn.functional as F
 
 from . import _ops
 from .rope import flat_freq_parts, wan_freqs
+
+# The rollout's GEMM solutions (hipBLASLt / rocBLAS), as torch's TunableOp
+# chose them on an MI355X for every GEMM shape of the rollout (written by
+# `python bench.py --tune-gemms`).  Its first lines pin the torch, HIP,
+# hipBLASLt and rocBLAS versions and the GPU architecture.
+GEMM_TUNING_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_tuning_gfx950.csv")
+
+
+def use_tuned_gemms(path: str = GEMM_TUNING_FILE) -> bool:
+    """Select GEMM solutions from a TunableOp results file (process-wide,
+    torch.cuda.tunable, tuning off).  Shapes the file does not list, and
+    every shape when its validator lines do not match this process's
+    libraries, keep torch's default choice.  Returns whether the file was
+    read."""
+    import torch.cuda.tunable as tunable
+    if not os.path.exists(path):
+        return False
+    tunable.enable(True)
+    tunable.tuning_enable(False)
+    return bool(tunable.read_file(path))
 
 
 @dataclass
