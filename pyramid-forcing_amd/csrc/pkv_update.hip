@@ -2018,6 +2018,37 @@ __device__ inline void veil_advance(VeilWords &v, const VeilStep &s) {
 // per call adds them: the results equal F calls of one frame bit for bit.
 constexpr int kEfRing = 2;
 
+// Groups per workgroup of evict_frames_kernel: the workgroups of one call
+// all run at once, three per compute unit, and those on a unit with three
+// take longer than those on a unit with two (one frame's copies at a time
+// per workgroup).  Of the tile sizes up to merge_tile_groups(D) whose
+// workgroups fit in one round, the one with the fewest groups on the
+// busiest unit (ties: the larger tile); at 12 heads of 420 groups on 256
+// units, 7 groups (720 workgroups, 21 groups per busiest unit) rather than
+// 8 (636, 24).
+static int frames_tile_groups(int H, int MTPA, int D) {
+  static int cus[64];
+  int dev = 0;
+  const int full = merge_tile_groups(D);
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return full;
+  if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 0;
+  const int64_t n_cu = cus[dev];
+  if (n_cu <= 0) return full;
+  int best = full;
+  int64_t best_load = -1;
+  for (int g = full; g >= (full + 1) / 2; --g) {
+    const int64_t wgs = static_cast<int64_t>(H) * ((MTPA + g - 1) / g);
+    if (wgs > 3 * n_cu) break;
+    const int64_t load = (wgs + n_cu - 1) / n_cu * g;
+    if (best_load < 0 || load < best_load) {
+      best_load = load;
+      best = g;
+    }
+  }
+  return best;
+}
+
 __global__ void __launch_bounds__(kUpdThreads)
     evict_frames_kernel(const HeadState *states, const int64_t *t_vals, const float *weights,
                         const int32_t *num_groups, const float *weight_sum, int32_t n_merge, int32_t mma, UpdArgs a) {
@@ -2057,9 +2088,14 @@ __global__ void __launch_bounds__(kUpdThreads)
   const int FSEQ = a.FSEQ, D = a.D, MTPA = a.MTPA, W = a.width;
   const int cols = W / p, grid_ng = FSEQ / (p * p);
   const pkv_merge_layer &ml = a.ml;
-  const MergeLane ln(a, tile);
-  const int g = ln.g, c = ln.c, is_v = uni(ln.is_v);  // wave-uniform: a scalar buffer resource, no per-lane loop
-  const bool own = ln.own;
+  // a tile is gpt groups (the host's choice, at most merge_tile_groups(D)):
+  // lanes of the wave pairs' groups past gpt idle (no copies, no writes)
+  const int cpt = D / 8, gpw = 64 / cpt;
+  const int gpt = (MTPA + n_merge - 1) / n_merge;
+  const int local = (wave >> 1) * gpw + lane / cpt;
+  const int g = tile * gpt + local, c = (lane % cpt) * 8;
+  const int is_v = uni(wave & 1);  // wave-uniform: a scalar buffer resource, no per-lane loop
+  const bool own = lane / cpt < gpw && local < gpt && g < MTPA;
   const bool meta_lane = own && !is_v && c == 0;  // writes the group's count and positions
   // the group's members in every frame, copied into this wave's ring
   // slots in LDS (the dynamic LDS, which only the fallback path uses
@@ -2081,8 +2117,11 @@ __global__ void __launch_bounds__(kUpdThreads)
   {
     const int gc = min(g, grid_ng - 1);
     const int gbase = (gc / cols) * p * W + (gc % cols) * p;
+    // an idle lane's offset lies past the resource's end (the frames' bytes
+    // are below 2^31): its copies read zeros and fetch nothing
 #pragma unroll
-    for (int m = 0; m < kTok; ++m) toff[m] = c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb;
+    for (int m = 0; m < kTok; ++m)
+      toff[m] = local < gpt ? c * 2 + (gbase + (m / p) * W + m % p) * a.src_tb : 0x80000000u;
   }
   const int wave_s = uni(wave);
   typedef __attribute__((address_space(3))) char lds_char_t;
@@ -2684,7 +2723,8 @@ int pkv_evict_merge(uint8_t *states, int32_t H, int32_t F, int32_t FSEQ, int32_t
                     FSEQ / 4 <= MTPA && FSEQ <= kEvMaxFseq && D >= 8 * kPreTok && al16(new_k) && al16(new_v) &&
                     al16(ml->accum_sum_k) && al16(ml->accum_sum_v) && al16(ml->accum_group_ids);
   const bool one = grid && F == 1, many = grid && F > 1;
-  const int gpt = one ? evict_tile_groups(D) : merge_tile_groups(D);
+  int gpt = one ? evict_tile_groups(D) : merge_tile_groups(D);
+  if (many) gpt = frames_tile_groups(H, MTPA, D);
   u.n_merge = (MTPA + gpt - 1) / gpt;
   const void *kern = one ? reinterpret_cast<const void *>(evict_kernel)
                          : many ? reinterpret_cast<const void *>(evict_frames_kernel)
