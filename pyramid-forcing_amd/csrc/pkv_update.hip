@@ -82,6 +82,12 @@ struct PosSrc {
 
 __device__ inline uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 __device__ inline void st16(uint16_t *p, uint4 v) { *reinterpret_cast<uint4 *>(p) = v; }
+// non-temporal 16-byte store (written through, not kept dirty in L2)
+__device__ inline void st16_nt(void *p, uint4 v) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
+}
 
 // ---------------------------------------------------------------------------
 // mega_state_update (standalone op)
@@ -2339,7 +2345,10 @@ __global__ void __launch_bounds__(kUpdThreads)
           ox.y = pack_bf16x2(ax[sl][2] * inv, ax[sl][3] * inv);
           ox.z = pack_bf16x2(ax[sl][4] * inv, ax[sl][5] * inv);
           ox.w = pack_bf16x2(ax[sl][6] * inv, ax[sl][7] * inv);
-          st16((is_v ? ml.merge_v : ml.merge_k) + (hp * MTPA + g) * D + c, ox);
+          // (non-temporal, as the sums below: results nothing in the launch
+          // reads again; kept dirty in L2 they were written back at the
+          // launch's end, after the last workgroup)
+          st16_nt((is_v ? ml.merge_v : ml.merge_k) + (hp * MTPA + g) * D + c, ox);
           if (meta_lane) {
             int64_t *mp = ml.merge_pos + (hp * MTPA + g) * 3;
             mp[0] = fresh[sl] ? tpos[sl] : apos[sl][0];
@@ -2369,8 +2378,10 @@ __global__ void __launch_bounds__(kUpdThreads)
       if (!(touched & (1u << sl))) continue;
       float *acc_sum = is_v ? ml.accum_sum_v : ml.accum_sum_k;
       float4 *ap = reinterpret_cast<float4 *>(acc_sum + ((hs0 + sl) * MTPA + g) * D + c);
-      ap[0] = make_float4(ax[sl][0], ax[sl][1], ax[sl][2], ax[sl][3]);
-      ap[1] = make_float4(ax[sl][4], ax[sl][5], ax[sl][6], ax[sl][7]);
+      st16_nt(ap, make_uint4(__float_as_uint(ax[sl][0]), __float_as_uint(ax[sl][1]), __float_as_uint(ax[sl][2]),
+                             __float_as_uint(ax[sl][3])));
+      st16_nt(ap + 1, make_uint4(__float_as_uint(ax[sl][4]), __float_as_uint(ax[sl][5]), __float_as_uint(ax[sl][6]),
+                                 __float_as_uint(ax[sl][7])));
     }
   }
   if (last) {
