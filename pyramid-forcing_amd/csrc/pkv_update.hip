@@ -1976,7 +1976,7 @@ __global__ void __launch_bounds__(kUpdThreads)
         ox.y = pack_bf16x2(ax[2] * inv, ax[3] * inv);
         ox.z = pack_bf16x2(ax[4] * inv, ax[5] * inv);
         ox.w = pack_bf16x2(ax[6] * inv, ax[7] * inv);
-        st16((is_v ? ml.merge_v : ml.merge_k) + (hp * MTPA + gj) * D + c, ox);
+        st16_nt((is_v ? ml.merge_v : ml.merge_k) + (hp * MTPA + gj) * D + c, ox);  // not read again in the call
         if (meta_lane) {
           int64_t *mp = ml.merge_pos + (hp * MTPA + gj) * 3;
           mp[0] = is_new ? t : apos[j][0];
