@@ -510,6 +510,29 @@ def test_attention_tail_tiles_vs_float64():
     _attn_check(q, k, v, cu_q, cu_k, B, H)
 
 
+def test_attention_partial_query_tiles_vs_float64():
+    """The 12-wave kernel's last query tiles of every length class: sequences
+    of 512 + t or t rows (t = 1 ... 511) leave last tiles of 1-96 rows (the
+    key-split tail items), 97-383 rows (the full-tile path with the waves past
+    the rows only copying) and full tiles; tails with fewer than 8 key tiles
+    (40 and 200 keys) take the full-tile path too; 43 x 12 pairs."""
+    rng = np.random.default_rng(67)
+    B, H = 43, 12
+    tails = [1, 8, 32, 33, 64, 72, 96, 100, 128, 129, 200, 448, 480, 511]
+    Lq = np.array([(512 if b % 3 else 0) + tails[b % len(tails)] for b in range(B)])
+    Lq[0] = 1024  # two full tiles, no tail
+    Lk = rng.integers(256, 2000, size=B * H)
+    Lk[:8] = [256, 257, 288, 1000, 1025, 1999, 40, 200]
+    cu_q = np.concatenate([[0], np.cumsum(Lq)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(Lk)]).astype(np.int32)
+    q = O.f32_to_bf16((rng.standard_normal((cu_q[-1], H, 128)) * 0.5).astype(np.float32))
+    k = O.f32_to_bf16((rng.standard_normal((cu_k[-1], 128)) * 0.5).astype(np.float32))
+    v = O.f32_to_bf16((rng.standard_normal((cu_k[-1], 128)) * 0.5).astype(np.float32))
+    for s_ in range(0, B * H, 17):
+        k[cu_k[s_] + Lk[s_] - 1] = O.f32_to_bf16(np.full(128, 3.0, np.float32))
+    _attn_check(q, k, v, cu_q, cu_k, B, H)
+
+
 def test_attention_rejects_causal_and_bad_head_dim():
     q = torch.zeros(4, 1, 128, dtype=torch.bfloat16, device=DEV)
     cu = torch.tensor([0, 4], dtype=torch.int32, device=DEV)
