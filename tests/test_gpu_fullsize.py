@@ -393,3 +393,27 @@ def test_config5_full_shape_rollout():
                 mtc[l, h, fin[h, f]] = ng
         assert np.array_equal(got_states[l], st), f"block {l}: state records differ from the policy's state machine"
     assert np.array_equal(to_np(ctx.mgr.merge_token_count()), mtc)
+    # attention over the rollout's own packed pyramid (after the noisy pass of chunk `chunks`), for the first
+    # and the last block: MegaCache.attend against float64 on 40 query rows of every (frame, head) sequence
+    start = chunks * 3 * shape.frame_seqlen
+    H, D, FS = shape.heads, shape.head_dim, shape.frame_seqlen
+    rows = np.random.default_rng(3).choice(FS, size=40, replace=False)
+    for l in (0, shape.num_blocks - 1):
+        q = (torch.randn(1, 3 * FS, H, D, generator=g, device=DEV) * 2.0).to(torch.bfloat16)
+        out = caches[l].attend(q, start)
+        cu_k = to_np(caches[l].attend_kv(start, 3)).astype(np.int64)
+        kf = O.bf16_to_f32(to_np(ctx.mgr.k_flat_out().view(-1, D))).astype(np.float64)
+        vf = O.bf16_to_f32(to_np(ctx.mgr.v_flat_out().view(-1, D))).astype(np.float64)
+        qf = O.bf16_to_f32(to_np(q[0])).astype(np.float64)
+        got = O.bf16_to_f32(to_np(out[0])).astype(np.float64)
+        errs = []
+        for f in range(3):
+            for h in range(H):
+                s_ = f * H + h
+                k_, v_ = kf[cu_k[s_]:cu_k[s_ + 1]], vf[cu_k[s_]:cu_k[s_ + 1]]
+                assert len(k_) > 0
+                want = O.attention_ref(qf[f * FS + rows, h], k_, v_)
+                errs.append(np.abs(got[f * FS + rows, h] - want))
+        err = np.concatenate(errs)
+        assert np.isfinite(got).all()
+        assert err.max() < 2e-2 and err.mean() < 2e-3, (l, err.max(), err.mean())
