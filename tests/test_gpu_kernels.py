@@ -395,6 +395,20 @@ def test_attention_large_launch_vs_float64(kv_per_head, H):
     _attn_check(q, k, v, cu_q, cu_k, 86, H, kv_per_head)
 
 
+@pytest.mark.parametrize("B", [86, 20])
+def test_attention_empty_query_sequences_vs_float64(B):
+    """Batches without query rows (Lq = 0) between others, in a launch of the
+    12-wave kernel (86 x 12 pairs) and of the 8-wave one (20 x 12): their
+    sequences have no work items and the other rows are unaffected."""
+    rng = np.random.default_rng(41)
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, True, B=B)
+    Lq = np.diff(cu_q)
+    Lq[[1, 7, B - 1]] = 0
+    cu_q = np.concatenate([[0], np.cumsum(Lq)]).astype(np.int32)
+    q = q[:cu_q[-1]]
+    _attn_check(q, k, v, cu_q, cu_k, B, 12)
+
+
 def test_attention_large_launch_strided_views_vs_float64():
     """Q, K, V and O as the first 128 columns of 256-wide rows (token and head
     strides of the views, K/V rows 512 bytes apart): the 12-wave kernel reads
