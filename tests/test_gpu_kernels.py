@@ -409,6 +409,22 @@ def test_attention_empty_query_sequences_vs_float64(B):
     _attn_check(q, k, v, cu_q, cu_k, B, 12)
 
 
+@pytest.mark.parametrize("B", [86, 20])
+def test_attention_longest_key_sequences_vs_float64(B):
+    """Sequences at the cache's largest key count (31 frames x 1,560 =
+    48,360 keys, the reference's max_seqlen_k) and beyond it (60,001) among
+    short ones, in both head_dim-128 kernels; their query rows against
+    float64."""
+    rng = np.random.default_rng(43)
+    q, k, v, cu_q, cu_k = _large_launch_case(rng, True, B=B)
+    Lk = np.diff(cu_k)
+    Lk[[3, 50 % len(Lk), len(Lk) - 2]] = [48360, 60001, 48360]
+    cu_k = np.concatenate([[0], np.cumsum(Lk)]).astype(np.int32)
+    k = O.f32_to_bf16((rng.standard_normal((cu_k[-1], 128)) * 0.5).astype(np.float32))
+    v = O.f32_to_bf16((rng.standard_normal((cu_k[-1], 128)) * 0.5).astype(np.float32))
+    _attn_check(q, k, v, cu_q, cu_k, B, 12)
+
+
 def test_attention_large_launch_strided_views_vs_float64():
     """Q, K, V and O as the first 128 columns of 256-wide rows (token and head
     strides of the views, K/V rows 512 bytes apart): the 12-wave kernel reads
